@@ -1,0 +1,122 @@
+"""ctypes binding of ``libd3d_hip.so``, the gfx950 kernels behind d3d_amd.
+
+The library is the product path: if it is missing, or a tensor is not on a
+HIP device, the calls below raise instead of falling back to CPU code.
+Build it with ``python -m d3d_amd.build``.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libd3d_hip.so")
+
+D3D_DTYPE_F32 = 0
+D3D_DTYPE_BF16 = 1
+D3D_INPUT_LOGITS = 0
+D3D_INPUT_PROBS = 1
+D3D_TOKEN_EMPTY_DISTRIBUTION = -1
+D3D_TOKEN_BAD_DRAFT = -2
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/d3d_hip.h.
+SIGNATURES = {
+    "d3d_status_string": (ctypes.c_char_p, [_I]),
+    "d3d_version": (_I, []),
+    "d3d_accept_workspace_bytes": (_SZ, [_I, _I, _I64]),
+    "d3d_accept_fused": (
+        _I,
+        [_P, _P, _I, _I, _P, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libd3d_hip.so once and declare every exported signature."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: run `python -m d3d_amd.build` (hipcc, gfx950)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise for a non-zero status: ValueError for argument errors, RuntimeError for HIP errors."""
+    if status == 0:
+        return
+    msg = load().d3d_status_string(status).decode()
+    if status < 0:
+        raise ValueError(f"{what}: {msg} (status {status})")
+    raise RuntimeError(f"{what}: HIP error {status}: {msg}")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def require_device(*tensors: Optional[torch.Tensor]) -> torch.device:
+    """All given tensors must live on one HIP device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "d3d_amd kernels run on a HIP device only; got a tensor on "
+                f"{t.device} (there is no CPU path)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise RuntimeError("no device tensor given")
+    return dev
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, key: str, nbytes: int) -> torch.Tensor:
+    """Workspace cached per (device, current stream, key).
+
+    One workspace per stream keeps calls on concurrent streams from sharing
+    scratch memory; calls on one stream are ordered, so reuse is safe.
+    """
+    sp = stream_ptr(device)
+    k = (device.index, sp, key)
+    ws = _workspaces.get(k)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[k] = ws
+    return ws
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return D3D_DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return D3D_DTYPE_BF16
+    raise ValueError(f"unsupported dtype {t.dtype}: expected float32 or bfloat16")

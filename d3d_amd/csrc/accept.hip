@@ -1,0 +1,820 @@
+// Fused speculative acceptance for gfx950.
+//
+// Three stream-ordered phases, no atomics and no cross-workgroup waits:
+//
+//   1. stats     grid (C, rows, B).  Workgroup (c, r, b) streams chunk c of
+//                row r of request b once (target rows 0..K, then draft rows
+//                0..K-1; greedy mode reads target rows only) and reduces it to
+//                (max z, sum exp(z - max z), max x, argmax) with z = x / T, or
+//                to a plain sum for probability inputs.
+//   2. decide    grid (C, B).  Every workgroup of request b merges the chunk
+//                statistics of all rows in one fixed order (so all of them
+//                reach the same bits), evaluates u_i <= min(1, p_i / max(q_i,
+//                1e-12)) at every position and finds the first reject.
+//                Workgroup 0 writes the outputs; in stochastic modes every
+//                workgroup then reduces chunk c of the selected row pair
+//                (residual max(p - q, 0), and p) to chunk sums.
+//   3. resample  grid (B), stochastic modes only.  Locates the chunk in which
+//                the inverse CDF crosses u * W and scans it entry by entry.
+//
+// The phases replace per-workgroup completion counters: on MI355X a
+// device-scope release per workgroup (L2 write-back across XCDs) and
+// same-address atomics serialise, and cost far more than two extra launches.
+//
+// Reference semantics (D3D repository):
+//   single/eval_sync.py:287-305           temperature softmax / greedy one-hot
+//   single/speculative_sampling.py:37-76  normalise, accept test (<=), first
+//                                         reject, bonus row, residual with the
+//                                         mass <= 1e-12 fallback, resample
+//   single/eval_sync.py:1223-1234         greedy leading-match acceptance
+//
+// Every reduction runs in one fixed order for a given (V, dtype), so outputs
+// are deterministic.  The stochastic draw replaces torch.multinomial with an
+// inverse CDF over the unnormalised weights driven by resample_u:
+// token = first t with C_t > u * W, else the last t with positive weight.
+#include "d3d_common.hpp"
+#include "../../include/d3d_hip.h"
+
+#include <limits.h>
+
+namespace d3d {
+namespace accept {
+
+constexpr int NT = 256;          // threads per workgroup (4 waves)
+constexpr int kChunk = 4096;     // vocabulary entries per chunk
+constexpr int L = kChunk / NT;   // entries per thread per chunk
+constexpr int kMaxK = 127;       // K+1 target rows + K draft rows <= 255
+constexpr int kMaxStatLds = 2048;  // RowStat entries staged in LDS per batch (32 KiB)
+// Phases 2 and 3 are latency-bound, so their chunks hold nv2 16-byte vectors
+// per thread (nv2 in 1..kMaxNv2), chosen per launch: few requests get fine
+// chunks (more workgroups, shorter per-thread chains), many requests get
+// coarse ones (fewer redundant row merges).
+constexpr int kMaxNv2 = 4;
+
+struct RowStat {
+    float m;     // max of z over the chunk (logits), 0 (probs)
+    float s;     // sum exp(z - m) (logits) or sum x (probs)
+    float xmax;  // max raw value
+    int arg;     // first index of xmax
+};
+
+struct Decision {
+    int n;  // first rejected position (K when all accepted)
+    int flags;
+    float Mt, St, Mq, Sq;  // row statistics of the selected target/draft rows
+    int pad0, pad1;
+};
+
+struct ResStat {
+    float r;     // sum of residual weights over the chunk
+    float p;     // sum of target probabilities over the chunk
+    int last_r;  // last index with positive residual (-1 if none)
+    int last_p;  // last index with positive probability (-1 if none)
+};
+
+enum : int { kFlagInvalid = 1 };
+
+enum Mode : int { kGreedy = 0, kLogits = 1, kProbs = 2 };
+
+struct Params {
+    const void* target;
+    const void* draft;
+    const int64_t* tokens;
+    const float* uniforms;
+    const float* resample_u;
+    float T;
+    int K;
+    int V;
+    int C;   // phase-1 chunks per row
+    int C2;  // phase-2/3 sub-chunks per row (NT 16-byte vectors each)
+    int nv2; // sub-chunks per phase-2 workgroup
+    RowStat* stats;  // [B][R][C], R = 2K+1 (target rows 0..K, draft rows K+1..2K)
+    Decision* dec;   // [B]
+    ResStat* rstats; // [B][C]
+    float* xtok;     // [B][R]: value of row r at its draft token (rows != K)
+    int32_t* accepted;
+    uint8_t* mask;
+    int64_t* out_token;
+    uint8_t* all_accepted;
+    int64_t* posterior;
+};
+
+template <int DT>
+struct Vec;
+template <>
+struct Vec<kF32> {
+    static constexpr int E = 4;
+    static constexpr size_t bytes = 4;
+};
+template <>
+struct Vec<kBF16> {
+    static constexpr int E = 8;
+    static constexpr size_t bytes = 2;
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ const void* row_ptr(const void* base, size_t row, int V) {
+    return static_cast<const char*>(base) + row * (size_t)V * Vec<DT>::bytes;
+}
+
+template <int DT>
+__device__ __forceinline__ float load_one(const void* row, int e) {
+    if constexpr (DT == kF32) {
+        return static_cast<const float*>(row)[e];
+    } else {
+        return bf16_bits_to_f32(static_cast<const uint16_t*>(row)[e]);
+    }
+}
+
+// Loads L entries of one row into x[]: x[j*E + k] holds entry
+// first + j*stride + k.  Entries at or beyond V read as FILL (-inf for logits,
+// 0 for probabilities), which leaves every reduction unchanged, so the
+// arithmetic loops carry no bounds checks.  STREAM marks a single-use read
+// (non-temporal hint).
+template <int DT, bool VEC, bool STREAM, int LT>
+__device__ __forceinline__ void load_tile(const void* row, int V, int first, int stride, float fill,
+                                          float (&x)[LT]) {
+    constexpr int E = Vec<DT>::E;
+#pragma unroll
+    for (int j = 0; j < LT / E; ++j) {
+        const int e0 = first + j * stride;
+        if (VEC && e0 + E <= V) {
+            if constexpr (DT == kF32) {
+                const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + e0);
+                const f32x4 v = STREAM ? __builtin_nontemporal_load(p) : *p;
+                x[j * E + 0] = v.x;
+                x[j * E + 1] = v.y;
+                x[j * E + 2] = v.z;
+                x[j * E + 3] = v.w;
+            } else {
+                const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + e0);
+                const u32x4 v = STREAM ? __builtin_nontemporal_load(p) : *p;
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    x[j * E + 2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
+                    x[j * E + 2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const int e = e0 + k;
+                x[j * E + k] = e < V ? load_one<DT>(row, e) : fill;
+            }
+        }
+    }
+}
+
+// As load_tile, for the first nv (runtime, <= LT/E) vectors only.
+template <int DT, bool VEC, int LT>
+__device__ __forceinline__ void load_tile_n(const void* row, int V, int first, int stride, int nv, float fill,
+                                            float (&x)[LT]) {
+    constexpr int E = Vec<DT>::E;
+#pragma unroll
+    for (int j = 0; j < LT / E; ++j) {
+        if (j >= nv) break;
+        const int e0 = first + j * stride;
+        if (VEC && e0 + E <= V) {
+            if constexpr (DT == kF32) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + e0);
+                x[j * E + 0] = v.x;
+                x[j * E + 1] = v.y;
+                x[j * E + 2] = v.z;
+                x[j * E + 3] = v.w;
+            } else {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + e0);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    x[j * E + 2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
+                    x[j * E + 2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const int e = e0 + k;
+                x[j * E + k] = e < V ? load_one<DT>(row, e) : fill;
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ int tile_index(int first, int stride, int l) {
+    constexpr int E = Vec<DT>::E;
+    return first + (l / E) * stride + (l % E);
+}
+
+template <Mode M>
+__device__ __forceinline__ constexpr float fill_value() {
+    return M == kProbs ? 0.f : -INFINITY;
+}
+
+// Probability of one entry given its row statistics: softmax(x / T) entry
+// exp(x / T - M) / S for logits, x / max(S, 1e-12) for probabilities.
+// inv_s is 1 / S (logits) or 1 / max(S, 1e-12) (probabilities).
+template <Mode M, bool UNIT_T>
+__device__ __forceinline__ float prob_of(float x, float rowM, float inv_s, float T) {
+    if constexpr (M == kProbs) {
+        return x * inv_s;
+    } else {
+        return expf((UNIT_T ? x : x / T) - rowM) * inv_s;
+    }
+}
+
+template <Mode M>
+__device__ __forceinline__ float inv_sum(float S) {
+    return M == kProbs ? 1.0f / fmaxf(S, 1e-12f) : 1.0f / S;
+}
+
+__device__ __forceinline__ int wave_max_int(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_min_int(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int block_max_int(int v, int* scratch) {
+    v = wave_max_int(v);
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
+    __syncthreads();
+    int r = scratch[0];
+#pragma unroll
+    for (int k = 1; k < NT / kWave; ++k) r = max(r, scratch[k]);
+    return r;
+}
+
+__device__ __forceinline__ int block_min_int(int v, int* scratch) {
+    v = wave_min_int(v);
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
+    __syncthreads();
+    int r = scratch[0];
+#pragma unroll
+    for (int k = 1; k < NT / kWave; ++k) r = min(r, scratch[k]);
+    return r;
+}
+
+// ---------------------------------------------------------------- phase 1
+template <int DT, Mode M, bool UNIT_T>
+__device__ __forceinline__ RowStat chunk_stats(const float (&x)[L], int first, float T, bool want_arg,
+                                               float* rf, int* ri) {
+    constexpr int E = Vec<DT>::E;
+    float bv = x[0];
+    int bi = first;
+    if (want_arg) {
+        // Entries are visited in increasing index order, so ">" keeps the first max.
+#pragma unroll
+        for (int l = 1; l < L; ++l) {
+            if (x[l] > bv) {
+                bv = x[l];
+                bi = tile_index<DT>(first, NT * E, l);
+            }
+        }
+        block_argmax<NT>(bv, bi, rf, ri);
+    } else {
+#pragma unroll
+        for (int l = 1; l < L; ++l) bv = fmaxf(bv, x[l]);
+        bv = block_max<NT>(bv, rf);
+        bi = INT_MAX;
+    }
+    RowStat st;
+    st.xmax = bv;
+    st.arg = bi;
+    st.m = 0.f;
+    st.s = 0.f;
+    if constexpr (M == kProbs) {
+        float s = 0.f;
+#pragma unroll
+        for (int l = 0; l < L; ++l) s += x[l];
+        st.s = block_sum<NT>(s, rf);
+    } else if constexpr (M == kLogits) {
+        // max z equals (max x) / T: division by T > 0 is monotone.
+        const float m = UNIT_T ? bv : bv / T;
+        float s = 0.f;
+        if (m != -INFINITY) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) s += expf((UNIT_T ? x[l] : x[l] / T) - m);
+        }
+        st.m = m;
+        st.s = block_sum<NT>(s, rf);
+    }
+    return st;
+}
+
+template <int DT, bool VEC, Mode M>
+__global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
+    constexpr int E = Vec<DT>::E;
+    const int c = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
+    const int K = P.K, V = P.V, C = P.C, R = 2 * K + 1;
+    __shared__ float rf[NT / kWave];
+    __shared__ int ri[NT / kWave];
+
+    const void* row = r <= K ? row_ptr<DT>(P.target, (size_t)b * (K + 1) + r, V)
+                             : row_ptr<DT>(P.draft, (size_t)b * K + (r - K - 1), V);
+    // Draft token scored by this row (target row i and draft row i: token i).
+    const int ti = r < K ? r : r - K - 1;
+    int64_t tok = -1;
+    if (M != kGreedy && r != K && threadIdx.x == 0) tok = P.tokens[(size_t)b * K + ti];
+    const int first = c * kChunk + threadIdx.x * E;
+    float x[L];
+    load_tile<DT, VEC, true, L>(row, V, first, NT * E, fill_value<M>(), x);
+    const bool want_arg = r <= K;  // posterior needs target rows only
+    const RowStat st = P.T == 1.0f ? chunk_stats<DT, M, true>(x, first, P.T, want_arg, rf, ri)
+                                   : chunk_stats<DT, M, false>(x, first, P.T, want_arg, rf, ri);
+    if (threadIdx.x == 0) {
+        P.stats[((size_t)b * R + r) * C + c] = st;
+        // The workgroup whose chunk holds the token records its value once.
+        if (M != kGreedy && tok >= (int64_t)c * kChunk && tok < (int64_t)(c + 1) * kChunk && tok < V)
+            P.xtok[(size_t)b * R + r] = load_one<DT>(row, (int)tok);
+    }
+}
+
+// ---------------------------------------------------------------- phase 2
+constexpr int kLanesPerRow = 8;
+constexpr int kRowsPerPass = NT / kLanesPerRow;
+
+// Row statistics of request b: sM/sS per row (target rows 0..K, draft rows
+// K+1..2K) and sArg for target rows.  Chunk records are staged in LDS; 8
+// lanes per row then take every 8th chunk: first the row max (and argmax) by
+// a fold and a 3-step butterfly, then sum_c s_c * exp(m_c - M) with
+// independent exponentials, folded and butterflied the same way.
+template <Mode M>
+__device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, float* sS, int* sArg,
+                                           RowStat* lds) {
+    const int K = P.K, C = P.C, R = 2 * K + 1;
+    const int rows = M == kGreedy ? K + 1 : R;
+    const int g = threadIdx.x % kLanesPerRow;
+    const int batch_rows = min(rows, kMaxStatLds / C);  // >= 1: C <= kMaxStatLds
+    for (int r0 = 0; r0 < rows; r0 += batch_rows) {
+        const int nr = min(batch_rows, rows - r0);
+        const RowStat* src = P.stats + ((size_t)b * R + r0) * C;
+        __syncthreads();
+        for (int e = threadIdx.x; e < nr * C; e += NT) lds[e] = src[e];
+        __syncthreads();
+        for (int rr0 = 0; rr0 < nr; rr0 += kRowsPerPass) {
+            const int rr = rr0 + threadIdx.x / kLanesPerRow;
+            const bool live = rr < nr;
+            float m = -INFINITY, xm = -INFINITY;
+            int am = INT_MAX;
+            if (live) {
+                for (int k = g; k < C; k += kLanesPerRow) {
+                    const RowStat t = lds[rr * C + k];
+                    m = fmaxf(m, t.m);
+                    argmax_merge(xm, am, t.xmax, t.arg);
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < kLanesPerRow; o <<= 1) {
+                m = fmaxf(m, __shfl_xor(m, o, kWave));
+                const float x2 = __shfl_xor(xm, o, kWave);
+                const int a2 = __shfl_xor(am, o, kWave);
+                argmax_merge(xm, am, x2, a2);
+            }
+            float s = 0.f;
+            if (live && M != kGreedy) {
+                for (int k = g; k < C; k += kLanesPerRow) {
+                    const RowStat t = lds[rr * C + k];
+                    if constexpr (M == kProbs) {
+                        s += t.s;
+                    } else {
+                        if (t.m != -INFINITY) s += t.s * expf(t.m - m);
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o, kWave);
+            if (live && g == 0) {
+                sM[r0 + rr] = m;
+                sS[r0 + rr] = s;
+                if (r0 + rr <= K) sArg[r0 + rr] = am;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int DT, bool VEC, Mode M, bool UNIT_T>
+__device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowStat* lds, float* sM, float* sS,
+                                            int* sArg, uint8_t* sAcc, uint8_t* sBad, int* s_flags, float* rf,
+                                            int* ri) {
+    constexpr int E = Vec<DT>::E;
+    const int K = P.K, V = P.V, C = P.C;
+    const int tid = threadIdx.x;
+
+    // Independent loads first: tokens, uniforms and token values.
+    int64_t tok = 0;
+    float u = 0.f, xt = 0.f, xq = 0.f;
+    if (tid < K) {
+        tok = P.tokens[(size_t)b * K + tid];
+        if (M != kGreedy) {
+            u = P.uniforms[(size_t)b * K + tid];
+            xt = P.xtok[(size_t)b * (2 * K + 1) + tid];
+            xq = P.xtok[(size_t)b * (2 * K + 1) + K + 1 + tid];
+        }
+    }
+    merge_rows<M>(P, b, sM, sS, sArg, lds);
+
+    if (tid < K) {
+        const bool bad = tok < 0 || tok >= V;
+        bool acc = false;
+        if constexpr (M == kGreedy) {
+            acc = !bad && tok == (int64_t)sArg[tid];
+        } else {
+            if (!bad) {
+                const float pt = prob_of<M, UNIT_T>(xt, sM[tid], inv_sum<M>(sS[tid]), P.T);
+                const float qt = prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
+                const float a = fminf(1.0f, pt / fmaxf(qt, 1e-12f));
+                acc = u <= a;
+            }
+        }
+        sAcc[tid] = acc;
+        sBad[tid] = bad;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int n = K, bad = 0;
+        for (int p = 0; p < K; ++p) {
+            bad |= sBad[p];
+            if (!sAcc[p] && n == K) n = p;
+        }
+        s_flags[0] = n;
+        s_flags[1] = bad;
+    }
+    __syncthreads();
+    const int n = s_flags[0];
+    const bool bad = s_flags[1] != 0;
+
+    if (c == 0) {
+        for (int p = tid; p < K; p += NT) P.mask[(size_t)b * K + p] = sAcc[p];
+        if (P.posterior)
+            for (int r = tid; r <= K; r += NT) P.posterior[(size_t)b * (K + 1) + r] = sArg[r];
+        if (tid == 0) {
+            P.accepted[b] = bad ? 0 : n;
+            P.all_accepted[b] = !bad && n == K;
+            if (M == kGreedy || bad)
+                P.out_token[b] = bad ? (int64_t)D3D_TOKEN_BAD_DRAFT : (int64_t)sArg[n];
+            if (M != kGreedy) {
+                Decision d;
+                d.n = n;
+                d.flags = bad ? kFlagInvalid : 0;
+                d.Mt = sM[n];
+                d.St = sS[n];
+                d.Mq = n < K ? sM[K + 1 + n] : 0.f;
+                d.Sq = n < K ? sS[K + 1 + n] : 0.f;
+                d.pad0 = d.pad1 = 0;
+                P.dec[b] = d;
+            }
+        }
+    }
+    if constexpr (M != kGreedy) {
+        if (bad) return;
+        // Chunk sums of the selected row pair (reject row, or bonus row).
+        const bool res = n < K;
+        const void* trow = row_ptr<DT>(P.target, (size_t)b * (K + 1) + n, V);
+        const void* drow = res ? row_ptr<DT>(P.draft, (size_t)b * K + n, V) : nullptr;
+        const float Mt = sM[n], It = inv_sum<M>(sS[n]);
+        const float Mq = res ? sM[K + 1 + n] : 0.f, Iq = res ? inv_sum<M>(sS[K + 1 + n]) : 0.f;
+        // Workgroup c covers sub-chunks c*nv2 .. c*nv2+nv2-1; sub-chunk j is
+        // vector j of every thread (NT*E consecutive entries) and gets its own
+        // record, so phase 3 always scans one vector per thread.
+        constexpr int LM = kMaxNv2 * E;
+        const int nv2 = P.nv2;
+        const int first = c * (NT * E * nv2) + tid * E;
+        float xt[LM], xq[LM];
+        load_tile_n<DT, VEC, LM>(trow, V, first, NT * E, nv2, fill_value<M>(), xt);
+        if (res) load_tile_n<DT, VEC, LM>(drow, V, first, NT * E, nv2, fill_value<M>(), xq);
+        float rs[kMaxNv2], ps[kMaxNv2];
+        int lr[kMaxNv2], lp[kMaxNv2];
+#pragma unroll
+        for (int j = 0; j < kMaxNv2; ++j) {
+            rs[j] = ps[j] = 0.f;
+            lr[j] = lp[j] = -1;
+            if (j >= nv2) continue;
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const int l = j * E + k;
+                const int e = first + j * NT * E + k;
+                const float p = prob_of<M, UNIT_T>(xt[l], Mt, It, P.T);
+                ps[j] += p;
+                if (p > 0.f) lp[j] = e;
+                if (res) {
+                    const float r = fmaxf(p - prob_of<M, UNIT_T>(xq[l], Mq, Iq, P.T), 0.f);
+                    rs[j] += r;
+                    if (r > 0.f) lr[j] = e;
+                }
+            }
+        }
+        // One combined workgroup reduction for all sub-chunks.
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+#pragma unroll
+            for (int j = 0; j < kMaxNv2; ++j) {
+                rs[j] += __shfl_xor(rs[j], o, kWave);
+                ps[j] += __shfl_xor(ps[j], o, kWave);
+                lr[j] = max(lr[j], __shfl_xor(lr[j], o, kWave));
+                lp[j] = max(lp[j], __shfl_xor(lp[j], o, kWave));
+            }
+        }
+        __shared__ ResStat s_red[NT / kWave][kMaxNv2];
+        const int lane = tid & (kWave - 1), wv = tid / kWave;
+        if (lane == 0)
+#pragma unroll
+            for (int j = 0; j < kMaxNv2; ++j) s_red[wv][j] = ResStat{rs[j], ps[j], lr[j], lp[j]};
+        __syncthreads();
+        if (tid < nv2 && c * nv2 + tid < P.C2) {
+            ResStat st = s_red[0][tid];
+            for (int w = 1; w < NT / kWave; ++w) {
+                const ResStat t = s_red[w][tid];
+                st.r += t.r;
+                st.p += t.p;
+                st.last_r = max(st.last_r, t.last_r);
+                st.last_p = max(st.last_p, t.last_p);
+            }
+            P.rstats[(size_t)b * P.C2 + c * nv2 + tid] = st;
+        }
+    }
+}
+
+template <int DT, bool VEC, Mode M>
+__global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
+    __shared__ RowStat lds[kMaxStatLds];
+    __shared__ float sM[2 * kMaxK + 2], sS[2 * kMaxK + 2];
+    __shared__ int sArg[kMaxK + 1];
+    __shared__ uint8_t sAcc[kMaxK + 1], sBad[kMaxK + 1];
+    __shared__ int s_flags[2];
+    __shared__ float rf[NT / kWave];
+    __shared__ int ri[NT / kWave];
+    if (P.T == 1.0f)
+        decide_body<DT, VEC, M, true>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf, ri);
+    else
+        decide_body<DT, VEC, M, false>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf, ri);
+}
+
+// ---------------------------------------------------------------- phase 3
+// Inclusive scan over the workgroup in thread order (fixed order).
+__device__ __forceinline__ float block_incl_scan(float v, float* s_wave) {
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const float t = __shfl_up(v, o, kWave);
+        if (lane >= o) v += t;
+    }
+    __syncthreads();
+    if (lane == kWave - 1) s_wave[wv] = v;
+    __syncthreads();
+    float off = 0.f;
+    for (int k = 0; k < wv; ++k) off += s_wave[k];
+    return v + off;
+}
+
+template <int DT, bool VEC, Mode M, bool UNIT_T>
+__device__ __forceinline__ void resample_body(const Params& P, int b, float* s_wave, float* s_f, int* s_i,
+                                              int* ri) {
+    constexpr int E = Vec<DT>::E;
+    const int K = P.K, V = P.V, C = P.C2;
+    const int tid = threadIdx.x;
+    // All independent loads are issued before the first use.
+    const Decision d = P.dec[b];
+    const float v = P.resample_u[b];
+    ResStat mine0;  // this thread's chunk record of the first pass, reused below
+    mine0.r = mine0.p = 0.f;
+    mine0.last_r = mine0.last_p = -1;
+    if (tid < C) mine0 = P.rstats[(size_t)b * C + tid];
+    if (d.flags & kFlagInvalid) return;
+    const bool res = d.n < K;
+    const float It = inv_sum<M>(d.St), Iq = res ? inv_sum<M>(d.Sq) : 0.f;
+
+    // Chunk-level inverse CDF: inclusive scan of chunk sums in chunk order,
+    // the crossing chunk is the first whose inclusive sum exceeds v * W.
+    // Pass 1 picks the weights (residual unless its mass is <= 1e-12).
+    float WR = 0.f, WP = 0.f;
+    int LR = -1, LP = -1;
+    for (int c0 = 0; c0 < C; c0 += NT) {
+        float r = 0.f, p = 0.f;
+        if (c0 + tid < C) {
+            const ResStat t = c0 == 0 ? mine0 : P.rstats[(size_t)b * C + c0 + tid];
+            r = t.r;
+            p = t.p;
+            LR = max(LR, t.last_r);
+            LP = max(LP, t.last_p);
+        }
+        const float ir = block_incl_scan(r, s_wave);
+        const float ip = block_incl_scan(p, s_wave);
+        if (tid == NT - 1) {
+            s_f[0] = ir;
+            s_f[1] = ip;
+        }
+        __syncthreads();
+        WR += s_f[0];
+        WP += s_f[1];
+        __syncthreads();
+    }
+    LR = block_max_int(LR, ri);
+    LP = block_max_int(LP, ri);
+    const bool use_r = res && WR > 1e-12f;
+    const float W = use_r ? WR : WP;
+    const float target = v * W;
+    if (!(W > 0.f)) {
+        if (tid == 0) P.out_token[b] = D3D_TOKEN_EMPTY_DISTRIBUTION;
+        return;
+    }
+    int cs = INT_MAX;
+    float base = 0.f;
+    float carry = 0.f;
+    for (int c0 = 0; c0 < C && cs == INT_MAX; c0 += NT) {
+        float w = 0.f;
+        if (c0 + tid < C) {
+            const ResStat t = c0 == 0 ? mine0 : P.rstats[(size_t)b * C + c0 + tid];
+            w = use_r ? t.r : t.p;
+        }
+        const float incl = carry + block_incl_scan(w, s_wave);
+        const int mine = (c0 + tid < C && incl > target) ? c0 + tid : INT_MAX;
+        const int first = block_min_int(mine, ri);
+        if (first != INT_MAX && first == c0 + tid) s_f[2] = incl - w;
+        if (tid == NT - 1) s_f[3] = incl;
+        __syncthreads();
+        if (first != INT_MAX) {
+            cs = first;
+            base = s_f[2];
+        }
+        carry = s_f[3];
+        __syncthreads();
+    }
+    int token;
+    if (cs == INT_MAX) {
+        token = use_r ? LR : LP;
+    } else {
+        // Contiguous ownership: thread tid holds entries first..first+L-1.
+        // Sub-chunk cs: thread tid owns entries first..first+E-1.
+        const int first = cs * (NT * E) + tid * E;
+        float xt[E], xq[E];
+        load_tile<DT, VEC, false, E>(row_ptr<DT>(P.target, (size_t)b * (K + 1) + d.n, V), V, first, E,
+                                     fill_value<M>(), xt);
+        if (res)
+            load_tile<DT, VEC, false, E>(row_ptr<DT>(P.draft, (size_t)b * K + d.n, V), V, first, E,
+                                         fill_value<M>(), xq);
+        float w[E];
+        float tsum = 0.f;
+#pragma unroll
+        for (int l = 0; l < E; ++l) {
+            const float p = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
+            w[l] = use_r ? fmaxf(p - prob_of<M, UNIT_T>(xq[l], d.Mq, Iq, P.T), 0.f) : p;
+            tsum += w[l];
+        }
+        const float incl = block_incl_scan(tsum, s_wave);
+        float run = base + (incl - tsum);
+        int found = INT_MAX, lastpos = -1;
+#pragma unroll
+        for (int l = 0; l < E; ++l) {
+            run += w[l];
+            if (w[l] > 0.f) {
+                lastpos = first + l;
+                if (found == INT_MAX && run > target) found = first + l;
+            }
+        }
+        found = block_min_int(found, ri);
+        lastpos = block_max_int(lastpos, ri);
+        token = found != INT_MAX ? found : lastpos;
+    }
+    if (tid == 0) P.out_token[b] = token;
+}
+
+template <int DT, bool VEC, Mode M>
+__global__ __launch_bounds__(NT) void accept_resample_kernel(Params P) {
+    __shared__ float s_wave[NT / kWave];
+    __shared__ float s_f[4];
+    __shared__ int s_i[2];
+    __shared__ int ri[NT / kWave];
+    if (P.T == 1.0f)
+        resample_body<DT, VEC, M, true>(P, blockIdx.x, s_wave, s_f, s_i, ri);
+    else
+        resample_body<DT, VEC, M, false>(P, blockIdx.x, s_wave, s_f, s_i, ri);
+}
+
+struct Layout {
+    size_t stats, dec, rstats, xtok, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static int num_chunks(int64_t V) { return (int)((V + kChunk - 1) / kChunk); }
+// Vectors per thread in phase-2/3 chunks: aim for >= ~128 workgroups per
+// launch with as few redundant row merges as possible.
+static int pick_nv2(int B) { return B >= 4 ? 4 : (B >= 2 ? 2 : 1); }
+static int num_subchunks(int64_t V, int dtype) {
+    const int ch = NT * (dtype == D3D_DTYPE_F32 ? 4 : 8);
+    return (int)((V + ch - 1) / ch);
+}
+
+static Layout layout(int B, int K, int64_t V) {
+    Layout l;
+    const size_t C = (size_t)num_chunks(V), R = 2 * (size_t)K + 1;
+    const size_t C2 = (size_t)num_subchunks(V, D3D_DTYPE_F32);  // the larger count of the two dtypes
+    l.stats = 0;
+    l.dec = align256((size_t)B * R * C * sizeof(RowStat));
+    l.rstats = l.dec + align256((size_t)B * sizeof(Decision));
+    l.xtok = l.rstats + align256((size_t)B * C2 * sizeof(ResStat));
+    l.total = l.xtok + align256((size_t)B * R * sizeof(float));
+    return l;
+}
+
+template <int DT, bool VEC>
+static hipError_t launch(const Params& P, Mode mode, int B, hipStream_t stream) {
+    const dim3 block(NT);
+    const dim3 grid_dec(mode == kGreedy ? 1 : (P.C2 + P.nv2 - 1) / P.nv2, B);
+    switch (mode) {
+        case kGreedy:
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kGreedy>), dim3(P.C, P.K + 1, B), block, 0,
+                               stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kGreedy>), grid_dec, block, 0, stream, P);
+            return hipGetLastError();
+        case kLogits:
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kLogits>), dim3(P.C, 2 * P.K + 1, B), block, 0,
+                               stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kLogits>), grid_dec, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kLogits>), dim3(B), block, 0, stream, P);
+            return hipGetLastError();
+        default:
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kProbs>), dim3(P.C, 2 * P.K + 1, B), block, 0,
+                               stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kProbs>), grid_dec, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kProbs>), dim3(B), block, 0, stream, P);
+            return hipGetLastError();
+    }
+}
+
+}  // namespace accept
+}  // namespace d3d
+
+using namespace d3d;
+
+extern "C" size_t d3d_accept_workspace_bytes(int B, int K, int64_t V) {
+    if (B < 1 || K < 1 || V < 1) return 0;
+    return accept::layout(B, K, V).total;
+}
+
+extern "C" int d3d_accept_fused(const void* target, const void* draft, int dtype, int input_kind,
+                                const int64_t* draft_tokens, const float* uniforms,
+                                const float* resample_u, float temperature, int B, int K, int64_t V,
+                                int32_t* accepted, uint8_t* accept_mask, int64_t* out_token,
+                                uint8_t* all_accepted, int64_t* posterior, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+    using namespace accept;
+    if (B < 1 || B > 65535 || K < 1 || K > kMaxK || V < 1 || V > (int64_t)kMaxStatLds * kChunk)
+        return D3D_E_SHAPE;
+    if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
+    if (input_kind != D3D_INPUT_LOGITS && input_kind != D3D_INPUT_PROBS) return D3D_E_UNSUPPORTED;
+    const bool greedy = input_kind == D3D_INPUT_LOGITS && !(temperature > 1e-5f);
+    if (!target || !draft_tokens || !accepted || !accept_mask || !out_token || !all_accepted || !workspace)
+        return D3D_E_NULL;
+    if (!greedy && (!draft || !uniforms || !resample_u)) return D3D_E_NULL;
+    const Layout lay = layout(B, K, V);
+    if (workspace_bytes < lay.total) return D3D_E_WORKSPACE;
+
+    char* ws = static_cast<char*>(workspace);
+    Params P;
+    P.target = target;
+    P.draft = greedy ? nullptr : draft;
+    P.tokens = draft_tokens;
+    P.uniforms = uniforms;
+    P.resample_u = resample_u;
+    P.T = input_kind == D3D_INPUT_LOGITS ? temperature : 1.0f;
+    P.K = K;
+    P.V = (int)V;
+    P.C = num_chunks(V);
+    P.nv2 = pick_nv2(B);
+    P.C2 = num_subchunks(V, dtype);
+    P.stats = reinterpret_cast<RowStat*>(ws + lay.stats);
+    P.dec = reinterpret_cast<Decision*>(ws + lay.dec);
+    P.rstats = reinterpret_cast<ResStat*>(ws + lay.rstats);
+    P.xtok = reinterpret_cast<float*>(ws + lay.xtok);
+    P.accepted = accepted;
+    P.mask = accept_mask;
+    P.out_token = out_token;
+    P.all_accepted = all_accepted;
+    P.posterior = posterior;
+
+    const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;
+    const bool vec = ((uintptr_t)target % 16 == 0) && (greedy || (uintptr_t)draft % 16 == 0) &&
+                     ((size_t)V * esize) % 16 == 0;
+    const Mode mode = greedy ? kGreedy : (input_kind == D3D_INPUT_PROBS ? kProbs : kLogits);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (dtype == D3D_DTYPE_F32)
+        err = vec ? launch<kF32, true>(P, mode, B, s) : launch<kF32, false>(P, mode, B, s);
+    else
+        err = vec ? launch<kBF16, true>(P, mode, B, s) : launch<kBF16, false>(P, mode, B, s);
+    return err == hipSuccess ? D3D_OK : (int)err;
+}

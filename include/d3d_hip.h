@@ -1,0 +1,101 @@
+/*
+ * libd3d_hip -- C ABI of the MI355X (gfx950) kernels for D3D's per-step
+ * speculative hot path: fused acceptance, paged block-verify attention,
+ * KV append, diffusion-draft block attention and confidence/top-k unmask.
+ *
+ * Conventions shared by every entry point:
+ *  - All tensor arguments are device pointers to contiguous row-major data
+ *    owned by the caller.  The library allocates nothing.
+ *  - `stream` is a hipStream_t passed as void* (0 = the null stream).  Work is
+ *    enqueued on it; no entry point synchronises the host.
+ *  - Return value: 0 on success, a negative D3D_E_* code for an argument that
+ *    fails validation (nothing is launched), or a positive hipError_t when a
+ *    launch fails.
+ *  - Workspaces: size them with the matching *_workspace_bytes() call.  No
+ *    initialisation is needed; a workspace can be reused by later calls on
+ *    the same stream, but calls that share one workspace must not overlap
+ *    in time (use one workspace per stream).
+ */
+#ifndef D3D_HIP_H
+#define D3D_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of logits / probabilities. */
+#define D3D_DTYPE_F32 0
+#define D3D_DTYPE_BF16 1
+
+/* What the acceptance inputs hold. */
+#define D3D_INPUT_LOGITS 0 /* softmax(x / temperature); temperature <= 1e-5 selects greedy */
+#define D3D_INPUT_PROBS 1  /* (unnormalised) probabilities, divided by max(sum, 1e-12) */
+
+/* Status codes. */
+#define D3D_OK 0
+#define D3D_E_SHAPE (-1)
+#define D3D_E_DTYPE (-2)
+#define D3D_E_WORKSPACE (-3)
+#define D3D_E_NULL (-4)
+#define D3D_E_UNSUPPORTED (-5)
+
+/* Sentinels written to out_token[b] by the acceptance kernels. */
+#define D3D_TOKEN_EMPTY_DISTRIBUTION (-1) /* the resampling weights sum to zero */
+#define D3D_TOKEN_BAD_DRAFT (-2)          /* a draft token id lies outside [0, V) */
+
+/* Short description of a status code (static storage). */
+const char* d3d_status_string(int status);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int d3d_version(void);
+
+/*
+ * Bytes of workspace d3d_accept_fused needs for B requests of K draft tokens
+ * over a vocabulary of V entries (same for every dtype, input kind and mode).
+ */
+size_t d3d_accept_workspace_bytes(int B, int K, int64_t V);
+
+/*
+ * Fused acceptance for B independent requests in one HBM-streaming pass.
+ *
+ * Replaces, per request:
+ *   single/eval_sync.py:287-305        _sampling_probs (temperature softmax)
+ *   single/speculative_sampling.py:15-76 verify_speculative_block
+ *   single/eval_sync.py:1223-1234      greedy acceptance (cumprod of matches)
+ *   serving/engine.py:138-145          Engine._accepted
+ *
+ * target   [B, K+1, V]  rows 0..K-1 score draft token i, row K is the bonus row
+ * draft    [B, K, V]    proposal rows (unused in greedy mode; may be NULL)
+ * dtype    D3D_DTYPE_F32 or D3D_DTYPE_BF16 (both tensors)
+ * input_kind  D3D_INPUT_LOGITS or D3D_INPUT_PROBS
+ * draft_tokens [B, K] int64
+ * uniforms     [B, K] fp32 in [0, 1): position i accepted iff u_i <= a_i,
+ *              a_i = min(1, p_i(x_i) / max(q_i(x_i), 1e-12))
+ * resample_u   [B] fp32 in [0, 1): drives the inverse-CDF draw of the
+ *              correction (or bonus) token
+ * temperature  logits mode only; <= 1e-5 selects greedy acceptance
+ *              (uniforms, resample_u and draft unused, may be NULL)
+ *
+ * Outputs (device):
+ *   accepted     [B] int32  accepted draft tokens, 0..K
+ *   accept_mask  [B, K] uint8  the per-position decision at every position
+ *   out_token    [B] int64  correction token (or bonus token when all K are
+ *                accepted); D3D_TOKEN_* sentinels on invalid input
+ *   all_accepted [B] uint8
+ *   posterior    [B, K+1] int64  argmax of every target row (may be NULL)
+ */
+int d3d_accept_fused(const void* target, const void* draft, int dtype, int input_kind,
+                     const int64_t* draft_tokens, const float* uniforms,
+                     const float* resample_u, float temperature, int B, int K, int64_t V,
+                     int32_t* accepted, uint8_t* accept_mask, int64_t* out_token,
+                     uint8_t* all_accepted, int64_t* posterior, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* D3D_HIP_H */

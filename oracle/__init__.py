@@ -1,0 +1,167 @@
+"""ORACLE -- test infrastructure only.
+
+CPU restatements of D3D's per-step hot path, used as the checker for the
+gfx950 kernels.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package; the product
+(``d3d_amd``) never does.
+
+* ``accept_oracle.c`` (built into ``liboracle.so`` by ``oracle/Makefile``):
+  fp64 acceptance, greedy acceptance, inverse CDF, confidence/top-k unmask.
+* ``attention.py``: fp64 numpy paged attention (causal verify and
+  bidirectional draft block) over a logical gather of the pages.
+* ``torch_ref.py``: fp32 torch-CPU line-by-line restatement of
+  ``single/speculative_sampling.py`` with explicit uniforms (the CPU
+  baseline and a second, independently rounded check).
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+KIND_LOGITS = 0
+KIND_PROBS = 1
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile liboracle.so with gcc (via oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B", "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        P, I, L, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_double
+        lib.oracle_argmax_f32.restype = L
+        lib.oracle_argmax_f32.argtypes = [P, L]
+        lib.oracle_row_probs.restype = None
+        lib.oracle_row_probs.argtypes = [P, L, I, D, P]
+        lib.oracle_inverse_cdf.restype = L
+        lib.oracle_inverse_cdf.argtypes = [P, L, D, P]
+        lib.oracle_accept_dense.restype = None
+        lib.oracle_accept_dense.argtypes = [P, P, I, D, P, P, P, I, I, L, P, P, P, P, P, P]
+        lib.oracle_accept_sparse.restype = None
+        lib.oracle_accept_sparse.argtypes = [P, I, D, P, P, P, I, P, P, I, I, L, P, P, P, P, P, P]
+        lib.oracle_accept_greedy.restype = None
+        lib.oracle_accept_greedy.argtypes = [P, P, I, I, L, P, P, P, P, P]
+        lib.oracle_confidence_topk.restype = None
+        lib.oracle_confidence_topk.argtypes = [P, P, ctypes.c_int64, I, D, I, I, L, P, P]
+        _lib = lib
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _i64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int64))
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def argmax(x) -> int:
+    x = _f32(x)
+    return int(_load().oracle_argmax_f32(_p(x), x.size))
+
+
+def row_probs(x, kind: int = KIND_LOGITS, temperature: float = 1.0) -> np.ndarray:
+    x = _f32(x)
+    p = np.empty(x.size, dtype=np.float64)
+    _load().oracle_row_probs(_p(x), x.size, kind, float(temperature), _p(p))
+    return p
+
+
+def inverse_cdf(w, v: float):
+    """(token, margin) of the inverse-CDF draw over unnormalised fp64 weights."""
+    w = np.ascontiguousarray(np.asarray(w, dtype=np.float64))
+    m = np.zeros(1, dtype=np.float64)
+    t = _load().oracle_inverse_cdf(_p(w), w.size, float(v), _p(m))
+    return int(t), float(m[0])
+
+
+def accept_dense(target, draft, tokens, uniforms, resample_u, *, kind=KIND_LOGITS, temperature=1.0):
+    """fp64 dense acceptance; arrays [B,K+1,V], [B,K,V], [B,K], [B,K], [B]."""
+    t, d = _f32(target), _f32(draft)
+    tok, u, ru = _i64(tokens), _f32(uniforms), _f32(resample_u)
+    B, K1, V = t.shape
+    K = K1 - 1
+    out = dict(
+        accept_mask=np.zeros((B, K), np.uint8), accepted=np.zeros(B, np.int32),
+        out_token=np.zeros(B, np.int64), all_accepted=np.zeros(B, np.uint8),
+        u_margin=np.zeros(B, np.float64), cdf_margin=np.zeros(B, np.float64),
+    )
+    _load().oracle_accept_dense(
+        _p(t), _p(d), kind, float(temperature), _p(tok), _p(u), _p(ru), B, K, V,
+        _p(out["accept_mask"]), _p(out["accepted"]), _p(out["out_token"]),
+        _p(out["all_accepted"]), _p(out["u_margin"]), _p(out["cdf_margin"]),
+    )
+    return out
+
+
+def accept_sparse(target, tokens, q_ids, q_probs, uniforms, resample_u, *, kind=KIND_PROBS, temperature=1.0):
+    """fp64 sparse-proposal acceptance; q_ids/q_probs [B,K,S]."""
+    t, tok, qi, qp = _f32(target), _i64(tokens), _i64(q_ids), _f32(q_probs)
+    u, ru = _f32(uniforms), _f32(resample_u)
+    B, K1, V = t.shape
+    K, S = K1 - 1, qi.shape[2]
+    out = dict(
+        accept_mask=np.zeros((B, K), np.uint8), accepted=np.zeros(B, np.int32),
+        out_token=np.zeros(B, np.int64), all_accepted=np.zeros(B, np.uint8),
+        u_margin=np.zeros(B, np.float64), cdf_margin=np.zeros(B, np.float64),
+    )
+    _load().oracle_accept_sparse(
+        _p(t), kind, float(temperature), _p(tok), _p(qi), _p(qp), S, _p(u), _p(ru), B, K, V,
+        _p(out["accept_mask"]), _p(out["accepted"]), _p(out["out_token"]),
+        _p(out["all_accepted"]), _p(out["u_margin"]), _p(out["cdf_margin"]),
+    )
+    return out
+
+
+def accept_greedy(target, tokens):
+    """Greedy acceptance; target [B,K+1,V], tokens [B,K]."""
+    t, tok = _f32(target), _i64(tokens)
+    B, K1, V = t.shape
+    K = K1 - 1
+    out = dict(
+        posterior=np.zeros((B, K1), np.int64), accept_mask=np.zeros((B, K), np.uint8),
+        accepted=np.zeros(B, np.int32), out_token=np.zeros(B, np.int64),
+        all_accepted=np.zeros(B, np.uint8),
+    )
+    _load().oracle_accept_greedy(
+        _p(t), _p(tok), B, K, V, _p(out["posterior"]), _p(out["accept_mask"]),
+        _p(out["accepted"]), _p(out["out_token"]), _p(out["all_accepted"]),
+    )
+    return out
+
+
+def confidence_topk(logits, block, mask_id: int, k: int, temperature: float = 0.0):
+    """One unmask iteration; returns (new_block, x0, conf)."""
+    x = _f32(logits)
+    blk = _i64(block).copy()
+    B, Q, V = x.shape
+    x0 = np.zeros((B, Q), np.int64)
+    conf = np.zeros((B, Q), np.float32)
+    _load().oracle_confidence_topk(_p(x), _p(blk), int(mask_id), int(k), float(temperature),
+                                   B, Q, V, _p(x0), _p(conf))
+    return blk, x0, conf
+
+
+def num_transfer_tokens(num_masks: int, steps: int):
+    """single/eval_sync.py:440-444: even split, remainder to the first steps."""
+    steps = max(1, int(steps))
+    base, extra = divmod(int(num_masks), steps)
+    return [base + (1 if i < extra else 0) for i in range(steps)]

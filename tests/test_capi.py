@@ -1,0 +1,75 @@
+"""The C ABI library loads and exports every entry point include/d3d_hip.h declares.
+
+CPU only: no kernel is launched here.  Argument validation happens on the
+host before any HIP call, so invalid calls are exercised with null pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from d3d_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "d3d_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(d3d_\w+)\s*\(", text)))
+
+
+def test_header_declares_functions():
+    names = declared_functions()
+    assert "d3d_accept_fused" in names and len(names) >= 4
+
+
+def test_every_declared_function_is_exported_and_bound(d3d_lib):
+    for name in declared_functions():
+        assert hasattr(d3d_lib, name), f"{name} not exported by {_lib.LIB_PATH.name}"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_status_strings_and_version(d3d_lib):
+    assert d3d_lib.d3d_status_string(0) == b"ok"
+    assert b"shape" in d3d_lib.d3d_status_string(-1)
+    assert d3d_lib.d3d_version() >= 100
+
+
+def test_accept_workspace_bytes(d3d_lib):
+    small = d3d_lib.d3d_accept_workspace_bytes(1, 15, 151936)
+    big = d3d_lib.d3d_accept_workspace_bytes(8, 15, 151936)
+    assert 0 < small < big
+    assert d3d_lib.d3d_accept_workspace_bytes(0, 15, 100) == 0
+
+
+@pytest.mark.parametrize(
+    "B,K,V,dtype,kind,expect",
+    [
+        (0, 15, 100, 0, 0, -1),      # no requests
+        (1, 0, 100, 0, 0, -1),       # no draft tokens
+        (1, 128, 100, 0, 0, -1),     # K above the supported 127
+        (1, 15, 0, 0, 0, -1),        # empty vocabulary
+        (1, 15, 100, 7, 0, -2),      # unknown dtype
+        (1, 15, 100, 0, 9, -5),      # unknown input kind
+        (1, 15, 100, 0, 0, -4),      # null pointers
+    ],
+)
+def test_accept_rejects_invalid_arguments_without_launching(d3d_lib, B, K, V, dtype, kind, expect):
+    st = d3d_lib.d3d_accept_fused(None, None, dtype, kind, None, None, None, 1.0, B, K, V,
+                                  None, None, None, None, None, None, 0, None)
+    assert st == expect
+    with pytest.raises(ValueError):
+        _lib.check(st, "d3d_accept_fused")
+
+
+def test_accept_rejects_small_workspace(d3d_lib):
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    st = d3d_lib.d3d_accept_fused(p, p, 0, 0, p, p, p, 1.0, 1, 15, 151936,
+                                  p, p, p, p, None, p, 64, None)
+    assert st == -3

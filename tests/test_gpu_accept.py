@@ -1,0 +1,190 @@
+"""Parity of the fused acceptance kernel with the oracle (GPU).
+
+Integer outputs (accept mask, accepted length, correction/bonus token,
+posterior) must be bit-exact.  Stochastic cases are compared where the fp64
+oracle certifies the decision margins (|u - a| > 1e-5 at every position and
+the inverse-CDF crossing more than 1e-6 * W from both bar edges), so the
+result cannot depend on fp32 summation order; the fraction of certified
+cases is asserted to stay high.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from d3d_amd import speculative_sampling as ss
+from d3d_amd import workloads
+
+pytestmark = pytest.mark.gpu
+
+U_MARGIN = 1e-5
+CDF_MARGIN = 1e-6
+
+
+def _dev():
+    return torch.device("cuda:0")
+
+
+def _run(inp: workloads.AcceptInputs, temperature: float, dtype=torch.float32, kind="logits"):
+    dev = _dev()
+    t = inp.target.to(dev, dtype)
+    d = inp.draft.to(dev, dtype)
+    out = ss.accept_fused(t, d, inp.tokens.to(dev), temperature=temperature,
+                          uniforms=inp.uniforms.to(dev), resample_uniform=inp.resample_u.to(dev),
+                          input_kind=kind)
+    torch.cuda.synchronize()
+    return {k: getattr(out, k).cpu().numpy() for k in out._fields}, t.float().cpu(), d.float().cpu()
+
+
+def _check_stochastic(got, ref, min_certified=0.8):
+    ok = (ref["u_margin"] > U_MARGIN) & (ref["cdf_margin"] > CDF_MARGIN)
+    assert ok.mean() >= min_certified, f"only {ok.mean():.2f} of cases certified"
+    idx = np.flatnonzero(ok)
+    np.testing.assert_array_equal(got["accepted"][idx], ref["accepted"][idx])
+    np.testing.assert_array_equal(got["out_token"][idx], ref["out_token"][idx])
+    np.testing.assert_array_equal(got["all_accepted"][idx], ref["all_accepted"][idx].astype(bool))
+    np.testing.assert_array_equal(got["accept_mask"][idx], ref["accept_mask"][idx].astype(bool))
+    return idx
+
+
+@pytest.mark.parametrize("V", [1000, 4096, 4099, 10007, 151936])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_bit_exact(V, dtype):
+    inp = workloads.accept_inputs(11, B=4, K=15, V=V, temperature=0.0)
+    # make request 1 accept a prefix and request 2 accept everything
+    post = inp.target.to(dtype).float().argmax(-1)
+    inp.tokens[1, :6] = post[1, :6]
+    inp.tokens[2] = post[2, :15]
+    got, t, _ = _run(inp, 0.0, dtype)
+    ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
+    np.testing.assert_array_equal(got["posterior"], ref["posterior"])
+    np.testing.assert_array_equal(got["accepted"], ref["accepted"])
+    np.testing.assert_array_equal(got["out_token"], ref["out_token"])
+    np.testing.assert_array_equal(got["accept_mask"], ref["accept_mask"].astype(bool))
+    np.testing.assert_array_equal(got["all_accepted"], ref["all_accepted"].astype(bool))
+    assert got["accepted"][2] == 15 and got["accepted"][1] >= 6
+
+
+@pytest.mark.parametrize("V,B,K", [(1000, 8, 15), (4099, 4, 7), (32768, 2, 15), (151936, 8, 15)])
+@pytest.mark.parametrize("T", [1.0, 0.6])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_stochastic_logits_vs_oracle(V, B, K, T, dtype):
+    inp = workloads.accept_inputs(100 + V % 97 + B, B=B, K=K, V=V, temperature=T)
+    got, t, d = _run(inp, T, dtype)
+    ref = oracle.accept_dense(t.numpy(), d.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                              inp.resample_u.numpy(), kind=oracle.KIND_LOGITS, temperature=T)
+    _check_stochastic(got, ref, min_certified=0.75)
+    # posterior is the argmax of every target row in every mode
+    np.testing.assert_array_equal(got["posterior"], t.numpy().argmax(-1))
+
+
+@pytest.mark.parametrize("V", [64, 4096, 151936])
+def test_stochastic_probs_input_vs_oracle(V):
+    inp = workloads.accept_inputs(7, B=6, K=15, V=V)
+    tp = torch.softmax(inp.target, -1) * 3.0  # unnormalised probabilities
+    dp = torch.softmax(inp.draft, -1)
+    inp2 = workloads.AcceptInputs(tp, dp, inp.tokens, inp.uniforms, inp.resample_u)
+    got, t, d = _run(inp2, 1.0, kind="probs")
+    ref = oracle.accept_dense(t.numpy(), d.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                              inp.resample_u.numpy(), kind=oracle.KIND_PROBS)
+    _check_stochastic(got, ref, min_certified=0.66)
+
+
+def test_config0_fixture_seeds_bit_exact():
+    """Batch-1 acceptance at V=151936 (T=1) on 32 seeds, each request alone."""
+    certified = 0
+    for seed in range(32):
+        inp = workloads.accept_inputs(seed, B=1, K=15)
+        got, t, d = _run(inp, 1.0)
+        ref = oracle.accept_dense(t.numpy(), d.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                                  inp.resample_u.numpy(), kind=oracle.KIND_LOGITS, temperature=1.0)
+        if ref["u_margin"][0] > U_MARGIN and ref["cdf_margin"][0] > CDF_MARGIN:
+            certified += 1
+            assert got["accepted"][0] == ref["accepted"][0], seed
+            assert got["out_token"][0] == ref["out_token"][0], seed
+            np.testing.assert_array_equal(got["accept_mask"][0], ref["accept_mask"][0].astype(bool))
+    assert certified >= 28
+
+
+def test_equal_distributions_accept_all_and_draw_bonus_row():
+    V = 5000
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 4, V, generator=g)
+    x[:, 3] = -30.0
+    x[0, 3, 1234] = 30.0  # bonus row of request 0 is (numerically) one-hot
+    inp = workloads.AcceptInputs(x, x[:, :3].clone(), torch.randint(0, V, (2, 3), generator=g),
+                                 torch.rand(2, 3, generator=g), torch.rand(2, generator=g))
+    got, _, _ = _run(inp, 1.0)
+    assert list(got["accepted"]) == [3, 3] and got["all_accepted"].all()
+    assert got["out_token"][0] == 1234
+
+
+def test_bad_draft_token_is_reported_not_read():
+    inp = workloads.accept_inputs(5, B=3, K=4, V=512)
+    inp.tokens[1, 2] = 512
+    inp.tokens[2, 0] = -1
+    for T in (1.0, 0.0):
+        got, _, _ = _run(inp, T)
+        assert got["out_token"][1] == -2 and got["out_token"][2] == -2
+        assert got["out_token"][0] >= 0
+
+
+def test_empty_distribution_sentinel():
+    V = 300
+    t = torch.zeros(1, 2, V)
+    d = torch.full((1, 1, V), 1.0 / V)
+    inp = workloads.AcceptInputs(t, d, torch.tensor([[7]]), torch.tensor([[0.5]]), torch.tensor([0.5]))
+    got, _, _ = _run(inp, 1.0, kind="probs")
+    assert got["accepted"][0] == 0 and got["out_token"][0] == -1
+
+
+def test_u_equal_a_boundary_accepts_on_device():
+    V = 4
+    t = torch.tensor([[[0.25, 0.75, 0, 0], [0.25, 0.75, 0, 0]]])
+    d = torch.tensor([[[0.5, 0.5, 0, 0]]])
+    for u, expect in ((0.5, 1), (float(np.nextafter(np.float32(0.5), np.float32(1))), 0)):
+        inp = workloads.AcceptInputs(t, d, torch.tensor([[0]]), torch.tensor([[u]]), torch.tensor([0.1]))
+        got, _, _ = _run(inp, 1.0, kind="probs")
+        assert got["accepted"][0] == expect
+        if not expect:
+            assert got["out_token"][0] == 1
+
+
+def test_workspace_reuse_across_calls_and_shapes():
+    """Counters are left at zero: repeated calls of different sizes agree with the oracle."""
+    for B, V in ((8, 151936), (1, 4096), (3, 70000), (8, 151936)):
+        inp = workloads.accept_inputs(B * 7 + V % 13, B=B, K=15, V=V, temperature=0.0)
+        got, t, _ = _run(inp, 0.0)
+        ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
+        np.testing.assert_array_equal(got["posterior"], ref["posterior"])
+        np.testing.assert_array_equal(got["out_token"], ref["out_token"])
+
+
+def test_verify_speculative_block_reference_surface():
+    inp = workloads.accept_inputs(9, B=1, K=15)
+    dev = _dev()
+    p = torch.softmax(inp.target, -1).to(dev)
+    q = torch.softmax(inp.draft, -1).to(dev)
+    res = ss.verify_speculative_block(inp.tokens.to(dev), p, q, uniforms=inp.uniforms.to(dev),
+                                      resample_uniform=inp.resample_u.to(dev))
+    ref = oracle.accept_dense(p.cpu().numpy(), q.cpu().numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                              inp.resample_u.numpy(), kind=oracle.KIND_PROBS)
+    assert ref["u_margin"][0] > U_MARGIN and ref["cdf_margin"][0] > CDF_MARGIN
+    assert res.accepted_draft_tokens == ref["accepted"][0]
+    assert int(res.correction_token[0]) == ref["out_token"][0]
+    assert res.all_accepted == bool(ref["all_accepted"][0])
+    assert res.correction_token.shape == (1,) and res.correction_token.dtype == torch.int64
+    # reference-style call without uniforms still works
+    res2 = ss.verify_speculative_block(inp.tokens.to(dev), p, q)
+    assert 0 <= res2.accepted_draft_tokens <= 15
+    with pytest.raises(ValueError, match="batch size 1"):
+        ss.verify_speculative_block(inp.tokens.repeat(2, 1).to(dev), p.repeat(2, 1, 1), q.repeat(2, 1, 1))
+
+
+def test_cpu_tensors_are_rejected_loudly():
+    inp = workloads.accept_inputs(1, B=1, K=3, V=64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        ss.accept_fused(inp.target, inp.draft, inp.tokens, uniforms=inp.uniforms,
+                        resample_uniform=inp.resample_u)

@@ -1,0 +1,259 @@
+"""Pins the acceptance oracle (CPU only).
+
+The reference ships no golden vectors for this path, so the oracle is pinned
+by known-answer tests, closed forms, brute force, the rejection-sampling
+theorem (the first emitted token is distributed exactly as the target row),
+and agreement with an independently rounded fp32 torch restatement of
+single/speculative_sampling.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import torch_ref
+from d3d_amd import workloads
+
+pytestmark = pytest.mark.usefixtures("oracle_lib")
+
+
+def test_argmax_first_max_tie_rule():
+    assert oracle.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert oracle.argmax([-np.inf, -np.inf]) == 0
+    x = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
+    assert oracle.argmax(x) == int(torch.from_numpy(x).argmax())
+
+
+def test_row_probs_matches_closed_form_softmax():
+    x = np.random.default_rng(1).standard_normal(257).astype(np.float32) * 3
+    for T in (1.0, 0.7, 2.5):
+        z = x.astype(np.float64) / T
+        ref = np.exp(z - z.max())
+        ref /= ref.sum()
+        np.testing.assert_allclose(oracle.row_probs(x, oracle.KIND_LOGITS, T), ref, rtol=1e-12, atol=0)
+
+
+def test_row_probs_greedy_is_one_hot_at_first_max():
+    x = np.array([0.0, 5.0, 5.0, 1.0], np.float32)
+    np.testing.assert_array_equal(oracle.row_probs(x, oracle.KIND_LOGITS, 0.0), [0, 1, 0, 0])
+
+
+def test_row_probs_probs_kind_normalises_and_clamps():
+    np.testing.assert_allclose(oracle.row_probs([1, 3, 0, 4], oracle.KIND_PROBS), [0.125, 0.375, 0, 0.5])
+    np.testing.assert_array_equal(oracle.row_probs([0, 0, 0], oracle.KIND_PROBS), [0, 0, 0])
+
+
+def test_inverse_cdf_known_answers_and_brute_force():
+    for v in (0.0, 0.3, 0.999999):
+        assert oracle.inverse_cdf([0, 0, 5, 0], v)[0] == 2
+    assert oracle.inverse_cdf([0, 0, 0], 0.5)[0] == -1
+    assert oracle.inverse_cdf([1, 1, 1, 1], 0.5)[0] == 2  # C_1 = 2 is not > 2
+    assert oracle.inverse_cdf([1, 1, 1, 1], 0.49)[0] == 1
+    rng = np.random.default_rng(2)
+    for _ in range(200):
+        w = rng.random(17) * (rng.random(17) > 0.3)
+        if w.sum() == 0:
+            continue
+        v = rng.random()
+        cdf = np.cumsum(w)
+        expect = int(np.searchsorted(cdf, v * cdf[-1], side="right"))
+        assert oracle.inverse_cdf(w, v)[0] == expect
+
+
+def _one(target_rows, draft_rows, tokens, u, ru, kind=oracle.KIND_PROBS, T=1.0):
+    t = np.asarray(target_rows, np.float32)[None]
+    d = np.asarray(draft_rows, np.float32)[None]
+    return oracle.accept_dense(t, d, [tokens], [u], [ru], kind=kind, temperature=T)
+
+
+def test_accept_equal_distributions_always_accept_and_sample_bonus():
+    p = [0.1, 0.2, 0.3, 0.4]
+    bonus = [0.0, 0.0, 0.0, 1.0]
+    out = _one([p, p, bonus], [p, p], [1, 2], [0.999, 0.5], 0.42)
+    assert out["accepted"][0] == 2 and out["all_accepted"][0] == 1
+    assert out["out_token"][0] == 3
+    assert list(out["accept_mask"][0]) == [1, 1]
+
+
+def test_accept_boundary_u_equal_a_accepts():
+    # p_tok = 0.25, q_tok = 0.5 -> a = 0.5 exactly
+    p = [0.25, 0.75, 0.0, 0.0]
+    q = [0.5, 0.5, 0.0, 0.0]
+    assert _one([p, p], [q], [0], [0.5], 0.1)["accepted"][0] == 1
+    out = _one([p, p], [q], [0], [np.nextafter(np.float32(0.5), np.float32(1))], 0.1)
+    assert out["accepted"][0] == 0 and out["all_accepted"][0] == 0
+    # residual max(p - q, 0) = [0, .25, 0, 0] -> token 1 whatever the uniform
+    assert out["out_token"][0] == 1
+
+
+def test_accept_zero_q_token_is_clamped_and_accepts():
+    p = [0.5, 0.5, 0, 0]
+    q = [0.0, 1.0, 0, 0]
+    assert _one([p, p], [q], [0], [0.99], 0.3)["accepted"][0] == 1
+
+
+def test_accept_zero_p_token_accepts_only_at_u_zero():
+    p = [0.0, 1.0, 0, 0]
+    q = [0.5, 0.5, 0, 0]
+    assert _one([p, p], [q], [0], [0.0], 0.3)["accepted"][0] == 1
+    out = _one([p, p], [q], [0], [1e-7], 0.3)
+    assert out["accepted"][0] == 0 and out["out_token"][0] == 1
+
+
+def test_accept_first_reject_stops_scan_but_mask_reports_every_position():
+    p_ok = [0.5, 0.5, 0, 0]
+    q_bad = [0.0, 0.0, 1.0, 0.0]  # token 2 has p = 0: rejected for u > 0
+    rows_t = [p_ok, p_ok, p_ok, p_ok]
+    rows_d = [p_ok, q_bad, p_ok]
+    out = _one(rows_t, rows_d, [0, 2, 1], [0.3, 0.3, 0.3], 0.6)
+    assert out["accepted"][0] == 1
+    assert list(out["accept_mask"][0]) == [1, 0, 1]
+    # residual at position 1: max(p - q, 0) = [.5, .5, 0, 0]; v = .6 -> token 1
+    assert out["out_token"][0] == 1
+
+
+def test_accept_all_zero_target_gives_empty_distribution():
+    z = [0.0, 0.0, 0.0, 0.0]
+    out = _one([z, z], [[0.25] * 4], [0], [0.5], 0.5)
+    assert out["accepted"][0] == 0 and out["out_token"][0] == -1
+
+
+def test_accept_peaked_distributions_decide_independently_of_u():
+    # Construction of the SGLang known-answer test: one-hot target rows.
+    V = 8
+    t = np.zeros((3, V), np.float32)
+    d = np.full((2, V), 1.0 / V, np.float32)
+    t[0, 3] = t[1, 5] = t[2, 6] = 1.0
+    for u in (1e-6, 0.5, 0.999):
+        out = _one(t, d, [3, 4], [u, u], 0.77)
+        assert out["accepted"][0] == 1 and out["out_token"][0] == 5
+
+
+def test_rejection_sampling_theorem_first_token_is_target_distributed():
+    """P(first emitted token = t) = p_0(t) exactly, integrated over a u/v grid."""
+    rng = np.random.default_rng(3)
+    V, N = 6, 160
+    p = rng.random(V) ** 2
+    q = rng.random(V)
+    p /= p.sum()
+    q /= q.sum()
+    grid = (np.arange(N) + 0.5) / N
+    uu, vv = [a.ravel() for a in np.meshgrid(grid, grid, indexing="ij")]
+    M = uu.size
+    target = np.broadcast_to(np.stack([p, p]).astype(np.float32), (M, 2, V))
+    draft = np.broadcast_to(q.astype(np.float32)[None], (M, 1, V))
+    emitted = np.zeros(V)
+    for x in range(V):
+        out = oracle.accept_dense(target, draft, np.full((M, 1), x), uu[:, None], vv,
+                                  kind=oracle.KIND_PROBS)
+        first = np.where(out["accepted"] == 1, x, out["out_token"])
+        emitted += q[x] * np.bincount(first, minlength=V) / M
+    np.testing.assert_allclose(emitted, p, atol=2.5 / N)
+
+
+def test_sparse_matches_dense_when_support_is_the_whole_vocabulary():
+    V, K = 32, 3
+    rng = np.random.default_rng(4)
+    t = rng.random((1, K + 1, V)).astype(np.float32)
+    d = rng.random((1, K, V)).astype(np.float32)
+    tok = rng.integers(0, V, (1, K))
+    u = rng.random((1, K)).astype(np.float32)
+    ru = rng.random(1).astype(np.float32)
+    ids = np.broadcast_to(rng.permutation(V), (1, K, V))
+    probs = np.take_along_axis(d, ids, axis=2)
+    a = oracle.accept_dense(t, d, tok, u, ru, kind=oracle.KIND_PROBS)
+    b = oracle.accept_sparse(t, tok, ids, probs, u, ru, kind=oracle.KIND_PROBS)
+    for key in ("accepted", "out_token", "accept_mask", "all_accepted"):
+        np.testing.assert_array_equal(a[key], b[key])
+
+
+def test_sparse_duplicate_support_ids_accumulate():
+    V = 4
+    t = np.array([[[0.5, 0.5, 0, 0], [0.5, 0.5, 0, 0]]], np.float32)
+    ids = np.array([[[0, 0, 1]]])
+    probs = np.array([[[0.25, 0.25, 0.5]]], np.float32)
+    # q(0) = 0.5 -> a = 1 (accept); with u > 1 impossible, check residual path
+    out = oracle.accept_sparse(t, [[0]], ids, probs, [[0.2]], [0.5], kind=oracle.KIND_PROBS)
+    assert out["accepted"][0] == 1
+    ids2 = np.array([[[1, 1, 2]]])
+    out = oracle.accept_sparse(t, [[1]], ids2, np.array([[[0.4, 0.4, 0.2]]], np.float32),
+                               [[0.7]], [0.5], kind=oracle.KIND_PROBS)
+    # q(1) = 0.8 -> a = 0.625 < 0.7: reject; residual = [.5, 0, 0, 0] -> token 0
+    assert out["accepted"][0] == 0 and out["out_token"][0] == 0
+
+
+def test_greedy_known_answers():
+    V = 10
+    post = [3, 7, 1, 9]  # argmax of rows 0..3
+    t = np.zeros((1, 4, V), np.float32)
+    for i, a in enumerate(post):
+        t[0, i, a] = 1.0
+    t[0, 2, 4] = 1.0  # tie in row 2: first max (index 1) wins
+    out = oracle.accept_greedy(t, [[3, 7, 1]])
+    assert out["accepted"][0] == 3 and out["out_token"][0] == 9 and out["all_accepted"][0] == 1
+    out = oracle.accept_greedy(t, [[3, 5, 1]])
+    assert out["accepted"][0] == 1 and out["out_token"][0] == 7
+    assert list(out["accept_mask"][0]) == [1, 0, 1]
+    assert list(out["posterior"][0]) == post
+
+
+def test_greedy_matches_torch_cumprod_restatement():
+    rng = np.random.default_rng(5)
+    t = rng.standard_normal((4, 6, 50)).astype(np.float32)
+    post = t.argmax(-1)
+    block = np.concatenate([np.zeros((4, 1), np.int64), post[:, :5].copy()], axis=1)
+    block[1, 3] = (block[1, 3] + 1) % 50
+    block[2, 1] = (block[2, 1] + 1) % 50
+    out = oracle.accept_greedy(t, block[:, 1:])
+    n, corr, _ = torch_ref.greedy(torch.from_numpy(t), torch.from_numpy(block))
+    np.testing.assert_array_equal(out["accepted"], n.numpy())
+    np.testing.assert_array_equal(out["out_token"], corr.numpy())
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_fp64_oracle_agrees_with_fp32_torch_restatement_at_full_vocab(seed):
+    inp = workloads.accept_inputs(seed, B=1, K=15)
+    p_t = torch_ref.sampling_probs(inp.target, 1.0)
+    p_d = torch_ref.sampling_probs(inp.draft, 1.0)
+    n, tok, all_acc, mask = torch_ref.verify_block(inp.tokens, p_t, p_d, inp.uniforms, float(inp.resample_u[0]))
+    out = oracle.accept_dense(inp.target.numpy(), inp.draft.numpy(), inp.tokens.numpy(),
+                              inp.uniforms.numpy(), inp.resample_u.numpy(),
+                              kind=oracle.KIND_LOGITS, temperature=1.0)
+    assert out["u_margin"][0] > 1e-5 and out["cdf_margin"][0] > 1e-6
+    assert out["accepted"][0] == n
+    assert out["out_token"][0] == tok
+    assert bool(out["all_accepted"][0]) == all_acc
+    np.testing.assert_array_equal(out["accept_mask"][0].astype(bool), mask.numpy())
+
+
+def test_confidence_topk_brute_force_and_ties():
+    rng = np.random.default_rng(6)
+    B, Q, V, mask_id = 3, 8, 40, 39
+    logits = rng.standard_normal((B, Q, V)).astype(np.float32)
+    logits[..., mask_id] = -10
+    block = np.full((B, Q), mask_id, np.int64)
+    block[0, 2] = 5
+    block[1, :4] = 7
+    new, x0, conf = oracle.confidence_topk(logits, block, mask_id, 3, 0.0)
+    for b in range(B):
+        z = logits[b].astype(np.float64)
+        c = 1.0 / np.exp(z - z.max(-1, keepdims=True)).sum(-1)
+        np.testing.assert_allclose(conf[b], c, rtol=1e-6)
+        masked = np.flatnonzero(block[b] == mask_id)
+        order = masked[np.argsort(-conf[b][masked], kind="stable")][:3]
+        expect = block[b].copy()
+        expect[order] = x0[b][order]
+        np.testing.assert_array_equal(new[b], expect)
+    # equal confidences: lowest indices win
+    flat = np.zeros((1, 4, 6), np.float32)
+    new, _, _ = oracle.confidence_topk(flat, np.full((1, 4), 5), 5, 2, 0.0)
+    np.testing.assert_array_equal(new[0], [0, 0, 5, 5])
+
+
+def test_transfer_schedule_closed_form():
+    assert oracle.num_transfer_tokens(16, 4) == [4, 4, 4, 4]
+    assert oracle.num_transfer_tokens(15, 4) == [4, 4, 4, 3]
+    assert oracle.num_transfer_tokens(5, 3) == [2, 2, 1]
+    assert oracle.num_transfer_tokens(3, 0) == [3]
