@@ -3,14 +3,17 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 One step is one pass of the hot path over one batch of synthetic input with
-inputs resident in HBM: the fused acceptance of a batch-1 block of 16 target
-rows and 15 draft rows over the 151,936-entry vocabulary (fp32 logits,
-temperature 1).  Prints ONE JSON line.
+inputs resident in HBM: block-verify attention of a batch-1 block of 16
+queries (Qwen3-8B GQA: 32 query / 8 KV heads, d 128, bf16) over a 2048-token
+prefix in a paged cache, then the fused acceptance of 16 target and 15 draft
+fp32 logit rows over the 151,936-entry vocabulary at temperature 1.  Prints
+ONE JSON line.
 
-The roofline entry is for the fused acceptance call (stats + resample
-kernels, one launch each): algorithmic bytes = (16 + 15) rows x V x 4 B =
-18,840,064 B per call, divided by the call's average duration from HIP events
-recorded on the launch stream around the timed steps.
+The roofline entry is for whichever of the two calls takes longer:
+acceptance algorithmic bytes = (16 + 15) rows x V x 4 B = 18,840,064 B;
+attention algorithmic bytes = K and V rows of 2064 tokens x 8 heads x 256 B
++ q and o + page table = 8,716,804 B; each divided by the call's average
+duration from HIP events recorded on the launch stream.
 
 The CPU baseline times the fp32 torch-CPU restatement of the reference
 acceptance (softmax of both logit blocks, then single/speculative_sampling.py
@@ -81,6 +84,45 @@ class AcceptStep:
         return rows * V * 4
 
 
+class AttnStep:
+    """Pre-bound paged attention call (verify: causal block; draft: bidirectional)."""
+
+    def __init__(self, lens, Q, Hq, Hkv, page_size, causal: bool, dev, seed=0, num_pages=None):
+        import math
+        from d3d_amd import _lib, workloads
+        self.lib = _lib.load()
+        kv = workloads.paged_kv(seed, lens, Hkv=Hkv, D=128, page_size=page_size, num_pages=num_pages,
+                                device="cuda")
+        self.kv = kv
+        self.q = workloads.queries(seed + 7, len(lens), Q, Hq=Hq, device="cuda")
+        B = len(lens)
+        self.out = torch.empty_like(self.q)
+        P = kv.k_cache.shape[0]
+        max_pages = kv.block_table.shape[1]
+        max_ctx = max(lens)
+        n = self.lib.d3d_attn_workspace_bytes(B, Q, Hq, Hkv, 128, page_size, max_ctx)
+        self.ws = torch.zeros(max(n, 256), dtype=torch.uint8, device=dev)
+        self.fn = self.lib.d3d_verify_attn_paged if causal else self.lib.d3d_draft_block_attn
+        self.args = (self.q.data_ptr(), kv.k_cache.data_ptr(), kv.v_cache.data_ptr(),
+                     kv.block_table.data_ptr(), kv.context_lens.data_ptr(), self.out.data_ptr(),
+                     B, Q, Hq, Hkv, 128, page_size, max_pages, P, 1.0 / math.sqrt(128), max_ctx,
+                     self.ws.data_ptr(), self.ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+        self._check = _lib.check
+        # Algorithmic work: every visible key/value row once, q in, o out, the page table.
+        kv_bytes = sum(c * Hkv * 128 * 2 * 2 for c in lens)
+        self.bytes = kv_bytes + 2 * B * Q * Hq * 128 * 2 + sum(-(-c // page_size) * 4 for c in lens)
+        flops = 0
+        for c in lens:
+            seen = sum(min(c, c - Q + i + 1) for i in range(Q)) if causal else Q * c
+            flops += 4 * Hq * 128 * seen
+        self.flops = flops
+
+    def __call__(self):
+        st = self.fn(*self.args)
+        if st:
+            self._check(st, "paged attention")
+
+
 def time_calls(fn, steps: int, warmup: int, dev) -> float:
     """Average milliseconds per call from events on the launch stream."""
     for _ in range(warmup):
@@ -97,16 +139,21 @@ def time_calls(fn, steps: int, warmup: int, dev) -> float:
 
 
 def cpu_baseline(seconds: float):
-    """fp32 torch-CPU restatement of the reference acceptance, batch 1, T = 1."""
+    """fp32 torch-CPU restatement of the same step: paged attention + acceptance."""
+    import math
     from d3d_amd import workloads
     from oracle import torch_ref
+    kv = workloads.paged_kv(1234, [2048 + 16], Hkv=8, D=128, page_size=16, num_pages=256)
+    q = workloads.queries(1234 + 7, 1, 16, Hq=32)
     inp = workloads.accept_inputs(1234, B=1, K=15)
     threads = torch.get_num_threads()
 
     def once():
+        torch_ref.paged_attention_sdpa(q, kv.k_cache, kv.v_cache, kv.block_table, kv.context_lens,
+                                       1.0 / math.sqrt(128), causal=True)
         p = torch_ref.sampling_probs(inp.target, 1.0)
-        q = torch_ref.sampling_probs(inp.draft, 1.0)
-        torch_ref.verify_block(inp.tokens, p, q, inp.uniforms, float(inp.resample_u[0]))
+        pq = torch_ref.sampling_probs(inp.draft, 1.0)
+        torch_ref.verify_block(inp.tokens, p, pq, inp.uniforms, float(inp.resample_u[0]))
 
     for _ in range(2):
         once()
@@ -116,9 +163,10 @@ def cpu_baseline(seconds: float):
         n += 1
     us = (time.perf_counter() - t0) / n * 1e6
     return {
-        "value": round(us, 1), "unit": "us/call", "cores": threads, "kind": "port",
-        "sample": f"{n} calls of batch-1 T=1 acceptance (16+15 rows x 151936 fp32 logits), "
-                  f"torch CPU fp32 restatement, {threads} threads",
+        "value": round(1e6 / us, 1), "unit": "steps/s", "us_per_step": round(us, 1), "cores": threads,
+        "kind": "port",
+        "sample": f"{n} steps of the same workload (fp32 SDPA over the gathered 2064-token paged "
+                  f"prefix + batch-1 T=1 acceptance), torch CPU fp32 restatement, {threads} threads",
     }
 
 
@@ -135,19 +183,43 @@ def main():
     torch.cuda.set_device(dev)
     from d3d_amd import workloads
 
+    # Headline step: block-verify attention (batch 1, Qwen3-8B GQA 32/8, d 128, K=16
+    # causal block over a 2048-token prefix in 16-token pages of a shuffled
+    # 256-page pool) followed by fused acceptance (16 target + 15 draft fp32
+    # rows over vocab 151936, T = 1).
+    attn = AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234, num_pages=256)
     inp = workloads.accept_inputs(1234, B=1, K=15, device="cuda")
-    step = AcceptStep(inp, 1.0, dev)
-    ms = time_calls(step, args.steps, args.warmup, dev)
-    nbytes = step.algorithmic_bytes()
-    gbps = nbytes / (ms * 1e-3) / 1e9
+    acc = AcceptStep(inp, 1.0, dev)
 
-    # Secondary figures (not the headline): greedy acceptance, batch-8 acceptance.
-    g_inp = workloads.accept_inputs(1234, B=1, K=15, temperature=0.0, device="cuda")
-    g_step = AcceptStep(g_inp, 0.0, dev)
+    def step():
+        attn()
+        acc()
+
+    ms = time_calls(step, args.steps, args.warmup, dev)
+    attn_ms = time_calls(attn, args.steps, args.warmup, dev)
+    acc_ms = time_calls(acc, args.steps, args.warmup, dev)
+    acc_gbps = acc.algorithmic_bytes() / (acc_ms * 1e-3) / 1e9
+    attn_gbps = attn.bytes / (attn_ms * 1e-3) / 1e9
+    attn_tflops = attn.flops / (attn_ms * 1e-3) / 1e12
+    # The dominant kernel is the acceptance call when it takes longer.
+    if acc_ms >= attn_ms:
+        roof = {"bound": "hbm", "achieved": round(acc_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(acc_gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "fused acceptance"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "verify attention"}
+
+    # Secondary figures: greedy acceptance, batch-8 acceptance, batch-8
+    # concurrent verify attention, batch-4 draft block attention.
+    g_step = AcceptStep(workloads.accept_inputs(1234, B=1, K=15, temperature=0.0, device="cuda"), 0.0, dev)
     g_ms = time_calls(g_step, args.steps, args.warmup, dev)
-    b8_inp = workloads.accept_inputs(1234, B=8, K=15, device="cuda")
-    b8_step = AcceptStep(b8_inp, 1.0, dev)
+    b8_step = AcceptStep(workloads.accept_inputs(1234, B=8, K=15, device="cuda"), 1.0, dev)
     b8_ms = time_calls(b8_step, args.steps, args.warmup, dev)
+    lens8 = [c + 16 for c in workloads.concurrent_context_lens(2024, B=8)]
+    v8 = AttnStep(lens8, 16, 32, 8, 16, True, dev, seed=2024)
+    v8_ms = time_calls(v8, args.steps, args.warmup, dev)
+    dr = AttnStep([1024 + 16] * 4, 16, 16, 8, 16, False, dev, seed=77)
+    dr_ms = time_calls(dr, args.steps, args.warmup, dev)
 
     out = {
         "metric": "accept-kernel us & HBM GB/s; verify-attn TFLOP/s; draft+verify steps/s at 1 GPU",
@@ -160,28 +232,32 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16 attention, f32 acceptance",
         "data": "synthetic",
         "config": {
-            "workload": "fused acceptance, batch 1, 16 target + 15 draft rows, vocab 151936, "
-                        "fp32 logits N(0,4), draft = target + N(0,0.25), T=1, seeded uniforms",
+            "workload": "block-verify attention (batch 1, 32/8 heads, d 128, 16-query causal block, "
+                        "2048-token prefix, 16-token pages, shuffled 256-page pool, bf16) + fused "
+                        "acceptance (16 target + 15 draft fp32 rows, vocab 151936, T=1, seeded uniforms)",
             "global_batch": 1,
             "draft_block": 16,
+            "prefix": 2048,
             "vocab": 151936,
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(gbps, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
-        },
-        "accept_us": round(ms * 1e3, 2),
+        "roofline": roof,
+        "verify_attn_us": round(attn_ms * 1e3, 2),
+        "verify_attn_gbps": round(attn_gbps, 1),
+        "verify_attn_tflops": round(attn_tflops, 2),
+        "accept_us": round(acc_ms * 1e3, 2),
+        "accept_gbps": round(acc_gbps, 1),
         "accept_greedy_us": round(g_ms * 1e3, 2),
         "accept_greedy_gbps": round(g_step.algorithmic_bytes() / (g_ms * 1e-3) / 1e9, 1),
         "accept_b8_us": round(b8_ms * 1e3, 2),
         "accept_b8_gbps": round(b8_step.algorithmic_bytes() / (b8_ms * 1e-3) / 1e9, 1),
+        "verify_attn_b8_us": round(v8_ms * 1e3, 2),
+        "verify_attn_b8_gbps": round(v8.bytes / (v8_ms * 1e-3) / 1e9, 1),
+        "verify_attn_b8_tflops": round(v8.flops / (v8_ms * 1e-3) / 1e12, 2),
+        "draft_attn_b4_us": round(dr_ms * 1e3, 2),
+        "draft_attn_b4_gbps": round(dr.bytes / (dr_ms * 1e-3) / 1e9, 1),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -36,6 +36,16 @@ SIGNATURES = {
         _I,
         [_P, _P, _I, _I, _P, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
+    "d3d_attn_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
+    "d3d_verify_attn_paged": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
+    "d3d_draft_block_attn": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
+    "d3d_kv_append": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -1,0 +1,599 @@
+// Paged block attention for gfx950: block-verify (causal within the block)
+// and diffusion-draft block (bidirectional within the block) over a paged
+// KV cache, plus the KV append that precedes them.
+//
+// Reference behaviour (D3D repository):
+//   serving/vendor/ssd/layers/attention.py:21-22   KV append by slot mapping
+//   serving/vendor/ssd/layers/attention.py:38-41   flash_attn_with_kvcache(
+//       q, k_cache, v_cache, cache_seqlens, block_table, causal=True): query i
+//       of a block of Q sees keys j <= ctx - Q + i (bottom-right causal)
+//   serving/vendor/ssd/layers/attention.py:42-52 with serving/engine.py:41-42
+//       draft recovery: every block query sees keys j < ctx (prefix + block)
+//   models/d3d/modeling_d3d.py:190-200             GQA: head h reads KV head
+//       h / (Hq / Hkv)
+//
+// Layouts (bf16): q and out [B, Q, Hq, D]; caches [num_pages, page, Hkv, D]
+// (the reference's layout, serving/backend.py:46-48); block_table
+// [B, max_pages] int32; context_lens [B] int32 = prefix + Q (the block's own
+// keys are already appended).
+//
+// Work decomposition: workgroup (split, kv_head, b).  The G = Hq/Hkv query
+// heads of the group times the Q block queries form the MFMA rows (row
+// r = g*Q + qi, 16 rows per wave).  Each workgroup walks its split of the
+// context in 64-token tiles staged in LDS; all waves share a tile.  Scores
+// are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16: the
+// result layout (lane l holds tokens 4*(l/16)+r of row l%16) is, two 16-token
+// sub-tiles at a time, the A-operand layout the PV product needs, so
+// probabilities never leave registers.  V is read 4 columns at a time (one
+// 8-byte LDS read serves four 16-column output tiles), which permutes output
+// columns: tile (h, q) holds column 64h + 4j + q in lane column j.  Online softmax runs in the log2
+// domain.  With more than one split, (m, l, O) partials go to the workspace
+// and a combine kernel merges them.
+#include "d3d_common.hpp"
+#include "../../include/d3d_hip.h"
+
+#include <limits.h>
+
+namespace d3d {
+namespace attn {
+
+constexpr int D = 128;         // head dimension
+constexpr int TILE = 64;       // tokens per KV tile
+constexpr int ROWB = D * 2 + 16;  // LDS bytes per token row (16 B pad against bank conflicts)
+constexpr int kMaxWaves = 8;   // up to 128 MFMA rows per workgroup
+constexpr int kMaxSplitPages = 1024;  // page ids staged per split
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Params {
+    const uint16_t* q;
+    const uint16_t* k_cache;
+    const uint16_t* v_cache;
+    const int32_t* block_table;
+    const int32_t* context_lens;
+    uint16_t* out;
+    float* part_o;   // [B][Hkv][splits][M][D]
+    float* part_ml;  // [B][Hkv][splits][M][2]
+    int B, Q, Hq, Hkv, G, M;
+    int page_size, max_pages, num_pages;
+    int page_shift;  // log2(page_size) for powers of two, else -1
+    int split_tokens, num_splits;
+    float scale_log2;  // softmax scale * log2(e)
+};
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 pair -> packed bf16 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ s16x4 as_s16x4(uint32_t a, uint32_t b) {
+    u32x2 v = {a, b};
+    return __builtin_bit_cast(s16x4, v);
+}
+
+// Stages tokens [t0, t0 + TILE) of one KV head into registers.  Sixteen
+// threads cover one 256-byte token row (16-byte segment tid % 16); pass p of
+// NPASS handles token tid / 16 + p * (NT / 16), and each pass loads the
+// token's K and V segments (reg[p] and reg[NPASS + p]).  Tokens at or past
+// t_end, or on a page id outside the pool, load the split's first row (a
+// valid address) and are then zeroed, so masked probabilities (exactly 0)
+// never meet NaN or Inf garbage and no load is divergent.
+template <int NT>
+__device__ __forceinline__ void fetch_tile(const Params& P, int kvh, int t0, int t_begin, int t_end,
+                                           const int* pages, size_t safe_row, u32x4 (&reg)[2 * TILE * 16 / NT],
+                                           int& okmask) {
+    constexpr int NPASS = TILE * 16 / NT;
+    const int seg = threadIdx.x & 15;
+    const size_t row_elems = (size_t)P.Hkv * D;
+#pragma unroll
+    for (int pss = 0; pss < NPASS; ++pss) {
+        const int t = t0 + (int)(threadIdx.x >> 4) + pss * (NT / 16);
+        const int rel = t - t_begin;
+        const int pidx = P.page_shift >= 0 ? rel >> P.page_shift : rel / P.page_size;
+        const int slot = P.page_shift >= 0 ? t & (P.page_size - 1) : t % P.page_size;
+        const bool live = t < t_end;
+        const int page = live ? pages[live ? pidx : 0] : -1;  // index stays inside the split
+        const bool ok = page >= 0 && page < P.num_pages;
+        const size_t row = ok ? (size_t)(page * P.page_size + slot) : safe_row;
+        const size_t off = row * row_elems + (size_t)kvh * D + seg * 8;
+        reg[pss] = *reinterpret_cast<const u32x4*>(P.k_cache + off);
+        reg[NPASS + pss] = *reinterpret_cast<const u32x4*>(P.v_cache + off);
+        // Zeroing happens at store time so that this load is not waited on here.
+        okmask = pss == 0 ? (int)ok : (okmask | ((int)ok << pss));
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TILE * 16 / NT], int okmask) {
+    constexpr int NPASS = TILE * 16 / NT;
+    const int seg = threadIdx.x & 15;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int pss = 0; pss < NPASS; ++pss) {
+        const int tl = (int)(threadIdx.x >> 4) + pss * (NT / 16);
+        const bool ok = (okmask >> pss) & 1;
+        *reinterpret_cast<u32x4*>(lds + tl * ROWB + seg * 16) = ok ? reg[pss] : z;
+        *reinterpret_cast<u32x4*>(lds + TILE * ROWB + tl * ROWB + seg * 16) = ok ? reg[NPASS + pss] : z;
+    }
+}
+
+// Register budget: two workgroups per CU (two waves per SIMD) so that each
+// CU keeps 2 x DEPTH tiles of K/V in flight.
+template <int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
+    constexpr int NT = NW * 64;
+    const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g4 = lane >> 4, c16 = lane & 15;
+
+    __shared__ __attribute__((aligned(16))) char lds[2 * TILE * ROWB];
+    __shared__ int pages[kMaxSplitPages];
+
+    const int ctx = min(P.context_lens[b], P.max_pages * P.page_size);
+    const int t_begin = s * P.split_tokens;
+    const int t_end = min(t_begin + P.split_tokens, ctx);
+    // Page ids of the whole split in one round trip (split starts are page aligned).
+    const int p0 = t_begin / P.page_size;
+    const int np = t_end > t_begin ? (t_end - 1) / P.page_size - p0 + 1 : 0;
+    for (int i = threadIdx.x; i < np; i += NT) pages[i] = P.block_table[(size_t)b * P.max_pages + p0 + i];
+    __syncthreads();
+    // A row every masked lane may read: the first in-pool page of the split
+    // (or cache row 0).
+    size_t safe_row = 0;
+    for (int i = 0; i < np; ++i)
+        if (pages[i] >= 0 && pages[i] < P.num_pages) {
+            safe_row = (size_t)pages[i] * P.page_size;
+            break;
+        }
+
+    // This lane's query row for the Q^T operand and the softmax statistics.
+    const int row = w * 16 + c16;
+    const bool row_ok = row < P.M;
+    const int gh = row_ok ? row / P.Q : 0, qi = row_ok ? row % P.Q : 0;
+    const int head = kvh * P.G + gh;
+    // Largest key index this row may see.
+    const int limit = !row_ok ? -1 : (CAUSAL ? ctx - P.Q + qi : ctx - 1);
+    // Keys at or below limit_min are visible to every row of the workgroup.
+    const int limit_min = CAUSAL ? ctx - P.Q : ctx - 1;
+
+    // Q^T operand of v_mfma_f32_16x16x32_bf16: lane l holds row l%16, head
+    // dims 32*ks + 8*(l/16) + 0..7.  K is read with the same dim assignment,
+    // so the product sums over every dim whatever order the hardware uses.
+    bf16x8 qop[D / 32];
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row_ok)
+            v = *reinterpret_cast<const u32x4*>(P.q + (((size_t)b * P.Q + qi) * P.Hq + head) * D + ks * 32 + g4 * 8);
+        qop[ks] = __builtin_bit_cast(bf16x8, v);
+    }
+
+    f32x4 o[D / 16];
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) o[n] = {0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    // One 64-token tile from LDS into the running (m, l, O) of each row.
+    auto compute = [&](int t0) {
+        const char* kl = lds;
+        const char* vl = lds + TILE * ROWB;
+        // S^T sub-tiles: sc[m][r] = score of token t0 + 16m + 4*g4 + r for row c16.
+        float sc[TILE / 16][4];
+        {
+            // Four independent accumulation chains, interleaved.
+            f32x4 acc[TILE / 16];
+#pragma unroll
+            for (int m = 0; m < TILE / 16; ++m) acc[m] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < D / 32; ++ks) {
+                u32x4 kf[TILE / 16];
+#pragma unroll
+                for (int m = 0; m < TILE / 16; ++m)
+                    kf[m] = *reinterpret_cast<const u32x4*>(kl + (16 * m + c16) * ROWB + (ks * 32 + g4 * 8) * 2);
+#pragma unroll
+                for (int m = 0; m < TILE / 16; ++m)
+                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[m]), qop[ks], acc[m],
+                                                                   0, 0, 0);
+            }
+#pragma unroll
+            for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sc[m][r] = acc[m][r] * P.scale_log2;
+        }
+        // Masking only where the tile crosses the split end or the causal
+        // frontier of the earliest query (a uniform test).
+        if (t0 + TILE > min(t_end, limit_min + 1)) {
+#pragma unroll
+            for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = t0 + 16 * m + 4 * g4 + r;
+                    if (!(t <= limit && t < t_end)) sc[m][r] = -INFINITY;
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[m][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        // Rescale only when the running max of some row grows.
+        const float m_new = fmaxf(m_run, tmax);
+        const bool grow = m_new > m_run;
+        if (__any(grow)) {
+            const float alpha = grow ? (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new)) : 1.f;
+            l_run *= alpha;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float a = __shfl(alpha, 4 * g4 + r, 64);
+#pragma unroll
+                for (int n = 0; n < D / 16; ++n) o[n][r] *= a;
+            }
+            m_run = m_new;
+        }
+        // P as the A operand of 16x16x32: sub-tiles 2mp and 2mp+1 give the
+        // 8 token slots (4*g4 + r, then 16 + 4*g4 + r) of row c16.
+        uint32_t pw[TILE / 16][2];
+        float psum = 0.f;
+#pragma unroll
+        for (int m = 0; m < TILE / 16; ++m) {
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[r] = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[m][r] - m_run);
+                psum += p[r];
+            }
+            pw[m][0] = pack_bf16x2(p[0], p[1]);
+            pw[m][1] = pack_bf16x2(p[2], p[3]);
+        }
+        l_run += psum;
+#pragma unroll
+        for (int mp = 0; mp < TILE / 32; ++mp) {
+            const u32x4 pv = {pw[2 * mp][0], pw[2 * mp][1], pw[2 * mp + 1][0], pw[2 * mp + 1][1]};
+            const bf16x8 pop = __builtin_bit_cast(bf16x8, pv);
+#pragma unroll
+            for (int h = 0; h < D / 64; ++h) {
+                // V rows of the 8 token slots, 4 columns 64h + 4*c16 .. +3 each.
+                u32x2 vr[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int t = 32 * mp + 16 * (k >> 2) + 4 * g4 + (k & 3);
+                    vr[k] = *reinterpret_cast<const u32x2*>(vl + t * ROWB + (64 * h + 4 * c16) * 2);
+                }
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    // Column qq of each row: low or high half of word qq/2.
+                    const uint32_t sel = (qq & 1) ? 0x07060302u : 0x05040100u;
+                    const int word = qq >> 1;
+                    const u32x4 vw = {__builtin_amdgcn_perm(vr[1][word], vr[0][word], sel),
+                                      __builtin_amdgcn_perm(vr[3][word], vr[2][word], sel),
+                                      __builtin_amdgcn_perm(vr[5][word], vr[4][word], sel),
+                                      __builtin_amdgcn_perm(vr[7][word], vr[6][word], sel)};
+                    o[4 * h + qq] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, __builtin_bit_cast(bf16x8, vw),
+                                                                          o[4 * h + qq], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Tiles are staged global -> registers -> LDS; DEPTH register sets keep
+    // that many tiles in flight while the current one is computed.
+    constexpr int DEPTH = NW == 4 ? 2 : 1;
+    u32x4 regA[2 * TILE * 16 / NT];
+    int okA = 0;
+    if (t_begin < t_end) fetch_tile<NT>(P, kvh, t_begin, t_begin, t_end, pages, safe_row, regA, okA);
+    if constexpr (DEPTH == 1) {
+        for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
+            __syncthreads();
+            store_tile<NT>(lds, regA, okA);
+            __syncthreads();
+            if (t0 + TILE < t_end) fetch_tile<NT>(P, kvh, t0 + TILE, t_begin, t_end, pages, safe_row, regA, okA);
+            compute(t0);
+        }
+    } else {
+        u32x4 regB[2 * TILE * 16 / NT];
+        int okB = 0;
+        if (t_begin + TILE < t_end)
+            fetch_tile<NT>(P, kvh, t_begin + TILE, t_begin, t_end, pages, safe_row, regB, okB);
+        for (int t0 = t_begin; t0 < t_end; t0 += 2 * TILE) {
+            __syncthreads();
+            store_tile<NT>(lds, regA, okA);
+            __syncthreads();
+            if (t0 + 2 * TILE < t_end)
+                fetch_tile<NT>(P, kvh, t0 + 2 * TILE, t_begin, t_end, pages, safe_row, regA, okA);
+            compute(t0);
+            if (t0 + TILE < t_end) {
+                __syncthreads();
+                store_tile<NT>(lds, regB, okB);
+                __syncthreads();
+                if (t0 + 3 * TILE < t_end)
+                    fetch_tile<NT>(P, kvh, t0 + 3 * TILE, t_begin, t_end, pages, safe_row, regB, okB);
+                compute(t0 + TILE);
+            }
+        }
+    }
+
+    // Row sums: reduce the per-lane partials over the 4 lanes of a row.
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    if (P.num_splits == 1) {
+        const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int orow = w * 16 + 4 * g4 + r;
+            const float sc_r = __shfl(inv, 4 * g4 + r, 64);
+            if (orow < P.M) {
+                const int oh = kvh * P.G + orow / P.Q, oq = orow % P.Q;
+                uint16_t* dst = P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D;
+#pragma unroll
+                for (int h = 0; h < D / 64; ++h) {
+                    const u32x2 v = {pack_bf16x2(o[4 * h + 0][r] * sc_r, o[4 * h + 1][r] * sc_r),
+                                     pack_bf16x2(o[4 * h + 2][r] * sc_r, o[4 * h + 3][r] * sc_r)};
+                    *reinterpret_cast<u32x2*>(dst + 64 * h + 4 * c16) = v;
+                }
+            }
+        }
+    } else {
+        const size_t unit = ((size_t)b * P.Hkv + kvh) * P.num_splits + s;
+        float* po = P.part_o + unit * P.M * D;
+        float* pml = P.part_ml + unit * P.M * 2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int orow = w * 16 + 4 * g4 + r;
+            if (orow < P.M) {
+#pragma unroll
+                for (int h = 0; h < D / 64; ++h) {
+                    const f32x4 v = {o[4 * h + 0][r], o[4 * h + 1][r], o[4 * h + 2][r], o[4 * h + 3][r]};
+                    *reinterpret_cast<f32x4*>(po + (size_t)orow * D + 64 * h + 4 * c16) = v;
+                }
+            }
+        }
+        if (g4 == 0 && row_ok) {
+            pml[row * 2 + 0] = m_run;
+            pml[row * 2 + 1] = l_run;
+        }
+    }
+}
+
+// Merges the split partials: workgroup (row block, kv_head, b) handles
+// kRowsPerCombine rows; 32 threads per row, 4 columns each.  All split
+// statistics are loaded at once, then the weighted partial outputs.
+constexpr int kRowsPerCombine = 8;
+constexpr int kMaxSplits = 256;
+
+__global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
+    const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y, b = blockIdx.z;
+    const int S = P.num_splits;
+    const size_t unit0 = ((size_t)b * P.Hkv + kvh) * S;
+    __shared__ float wts[kRowsPerCombine][kMaxSplits];
+    __shared__ float lsum[kRowsPerCombine][kMaxSplits];
+    __shared__ float inv_den[kRowsPerCombine];
+    // Statistics of every (row, split) in one round trip.
+    for (int e = threadIdx.x; e < kRowsPerCombine * S; e += 256) {
+        const int rr = e / S, sp = e % S, row = r0 + rr;
+        float m = -INFINITY, l = 0.f;
+        if (row < P.M) {
+            const float2 ml = *reinterpret_cast<const float2*>(P.part_ml + ((unit0 + sp) * P.M + row) * 2);
+            m = ml.x;
+            l = ml.y;
+        }
+        wts[rr][sp] = m;
+        lsum[rr][sp] = l;
+    }
+    __syncthreads();
+    // One wave per row: lanes fold splits, then a butterfly (fixed order).
+    {
+        const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+        for (int rr = wv; rr < kRowsPerCombine; rr += 4) {
+            float mx = -INFINITY;
+            for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, wts[rr][sp]);
+            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            float den = 0.f;
+            for (int sp = lane; sp < S; sp += 64) {
+                const float m = wts[rr][sp];
+                const float w = (m == -INFINITY) ? 0.f : exp2f(m - mx);
+                wts[rr][sp] = w;
+                den += w * lsum[rr][sp];
+            }
+            for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+            if (lane == 0) inv_den[rr] = den > 0.f ? 1.f / den : 0.f;
+        }
+    }
+    __syncthreads();
+    const int rr = threadIdx.x / 32, c4 = (threadIdx.x % 32) * 4, row = r0 + rr;
+    if (row >= P.M) return;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int sp = 0; sp < S; ++sp) {
+        const float w = wts[rr][sp];
+        const f32x4 o = *reinterpret_cast<const f32x4*>(P.part_o + ((unit0 + sp) * P.M + row) * D + c4);
+        acc += w * o;
+    }
+    const float sc = inv_den[rr];
+    const int oh = kvh * P.G + row / P.Q, oq = row % P.Q;
+    const u32x2 v = {pack_bf16x2(acc[0] * sc, acc[1] * sc), pack_bf16x2(acc[2] * sc, acc[3] * sc)};
+    *reinterpret_cast<u32x2*>(P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D + c4) = v;
+}
+
+// KV append: one workgroup per token, 16 bytes per thread (K then V).
+__global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* k, const uint16_t* v, uint16_t* k_cache,
+                                                        uint16_t* v_cache, const int64_t* slots, int row_elems,
+                                                        int64_t num_slots) {
+    const int n = blockIdx.x;
+    const int64_t slot = slots[n];
+    if (slot < 0 || slot >= num_slots) return;
+    const int vecs = row_elems / 8;
+    for (int u = threadIdx.x; u < 2 * vecs; u += blockDim.x) {
+        const int kv = u / vecs, seg = u % vecs;
+        const uint16_t* src = (kv == 0 ? k : v) + (size_t)n * row_elems + seg * 8;
+        uint16_t* dst = (kv == 0 ? k_cache : v_cache) + (size_t)slot * row_elems + seg * 8;
+        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+    }
+}
+
+struct Plan {
+    int waves, split_tokens, num_splits;
+    bool valid;
+    size_t part_o_bytes, part_ml_bytes, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Split the context so that a launch has about kTargetWorkgroups workgroups,
+// in whole 64-token tiles.
+// Two workgroups are resident per CU (register-limited) on 256 CUs; twice
+// that many splits absorb requests whose context is shorter than the longest.
+constexpr int kTargetWorkgroups = 1024;
+
+static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
+    Plan p;
+    const int M = (Hq / Hkv) * Q;
+    p.waves = M <= 32 ? 2 : (M <= 64 ? 4 : 8);
+    const int tiles = (max_context + TILE - 1) / TILE;
+    const int units = B * Hkv;
+    int splits = (kTargetWorkgroups + units - 1) / units;
+    splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
+    splits = splits > kMaxSplits ? kMaxSplits : splits;
+    int tiles_per_split = (tiles + splits - 1) / splits;
+    // Split starts must be page aligned and a split's pages must fit in LDS.
+    const int unit_tokens = page_size % TILE == 0 ? page_size : (TILE % page_size == 0 ? TILE : TILE * page_size);
+    int split_tokens = tiles_per_split * TILE;
+    split_tokens = (split_tokens + unit_tokens - 1) / unit_tokens * unit_tokens;
+    while (split_tokens / page_size + 1 > kMaxSplitPages && split_tokens > unit_tokens) split_tokens -= unit_tokens;
+    p.split_tokens = split_tokens;
+    p.num_splits = (max_context + p.split_tokens - 1) / p.split_tokens;
+    if (p.num_splits < 1) p.num_splits = 1;
+    p.valid = p.num_splits <= kMaxSplits && p.split_tokens / page_size + 1 <= kMaxSplitPages;
+    if (p.num_splits == 1) {
+        p.part_o_bytes = p.part_ml_bytes = 0;
+    } else {
+        p.part_o_bytes = align256((size_t)B * Hkv * p.num_splits * M * D * sizeof(float));
+        p.part_ml_bytes = align256((size_t)B * Hkv * p.num_splits * M * 2 * sizeof(float));
+    }
+    p.total = p.part_o_bytes + p.part_ml_bytes;
+    if (p.total == 0) p.total = 256;
+    return p;
+}
+
+static int validate(int B, int Q, int Hq, int Hkv, int D_, int page_size, int max_pages, int num_pages,
+                    int max_context) {
+    if (B < 1 || B > 65535 || Q < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv) return D3D_E_SHAPE;
+    if (D_ != D) return D3D_E_UNSUPPORTED;
+    if ((Hq / Hkv) * Q > kMaxWaves * 16) return D3D_E_UNSUPPORTED;
+    if (page_size < 1 || max_pages < 1 || num_pages < 1 || max_context < 1) return D3D_E_SHAPE;
+    if ((int64_t)max_pages * page_size < max_context) return D3D_E_SHAPE;
+    return D3D_OK;
+}
+
+template <bool CAUSAL>
+static int run(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+               const int32_t* context_lens, void* out, int B, int Q, int Hq, int Hkv, int D_, int page_size,
+               int max_pages, int num_pages, float scale, int max_context, void* workspace, size_t ws_bytes,
+               void* stream) {
+    const int st = validate(B, Q, Hq, Hkv, D_, page_size, max_pages, num_pages, max_context);
+    if (st != D3D_OK) return st;
+    if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out) return D3D_E_NULL;
+    const Plan pl = plan(B, Q, Hq, Hkv, max_context, page_size);
+    if (!pl.valid) return D3D_E_UNSUPPORTED;
+    if (pl.num_splits > 1 && (!workspace || ws_bytes < pl.total)) return D3D_E_WORKSPACE;
+    Params P;
+    P.q = static_cast<const uint16_t*>(q);
+    P.k_cache = static_cast<const uint16_t*>(k_cache);
+    P.v_cache = static_cast<const uint16_t*>(v_cache);
+    P.block_table = block_table;
+    P.context_lens = context_lens;
+    P.out = static_cast<uint16_t*>(out);
+    P.part_o = pl.num_splits > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+    P.part_ml = pl.num_splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.part_o_bytes)
+                                  : nullptr;
+    P.B = B;
+    P.Q = Q;
+    P.Hq = Hq;
+    P.Hkv = Hkv;
+    P.G = Hq / Hkv;
+    P.M = P.G * Q;
+    P.page_size = page_size;
+    P.page_shift = -1;
+    if ((page_size & (page_size - 1)) == 0) {
+        int sh = 0;
+        while ((1 << sh) < page_size) ++sh;
+        P.page_shift = sh;
+    }
+    P.max_pages = max_pages;
+    P.num_pages = num_pages;
+    P.split_tokens = pl.split_tokens;
+    P.num_splits = pl.num_splits;
+    P.scale_log2 = scale * 1.4426950408889634f;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(pl.num_splits, Hkv, B);
+    switch (pl.waves) {
+        case 2:
+            hipLaunchKernelGGL((attn_split_kernel<2, CAUSAL>), grid, dim3(128), 0, s, P);
+            break;
+        case 4:
+            hipLaunchKernelGGL((attn_split_kernel<4, CAUSAL>), grid, dim3(256), 0, s, P);
+            break;
+        default:
+            hipLaunchKernelGGL((attn_split_kernel<8, CAUSAL>), grid, dim3(512), 0, s, P);
+            break;
+    }
+    if (pl.num_splits > 1)
+        hipLaunchKernelGGL(attn_combine_kernel, dim3((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B),
+                           dim3(256), 0, s, P);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}
+
+}  // namespace attn
+}  // namespace d3d
+
+using namespace d3d;
+
+extern "C" size_t d3d_attn_workspace_bytes(int B, int Q, int Hq, int Hkv, int D, int page_size,
+                                           int max_context) {
+    if (B < 1 || Q < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || D != attn::D || max_context < 1 || page_size < 1)
+        return 0;
+    return attn::plan(B, Q, Hq, Hkv, max_context, page_size).total;
+}
+
+extern "C" int d3d_verify_attn_paged(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_table, const int32_t* context_lens, void* out, int B,
+                                     int Q, int Hq, int Hkv, int D, int page_size, int max_pages, int num_pages,
+                                     float scale, int max_context, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    return attn::run<true>(q, k_cache, v_cache, block_table, context_lens, out, B, Q, Hq, Hkv, D, page_size,
+                           max_pages, num_pages, scale, max_context, workspace, workspace_bytes, stream);
+}
+
+extern "C" int d3d_draft_block_attn(const void* q, const void* k_cache, const void* v_cache,
+                                    const int32_t* block_table, const int32_t* context_lens, void* out, int B,
+                                    int Q, int Hq, int Hkv, int D, int page_size, int max_pages, int num_pages,
+                                    float scale, int max_context, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    return attn::run<false>(q, k_cache, v_cache, block_table, context_lens, out, B, Q, Hq, Hkv, D, page_size,
+                            max_pages, num_pages, scale, max_context, workspace, workspace_bytes, stream);
+}
+
+extern "C" int d3d_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
+                             const int64_t* slot_mapping, int n_tokens, int Hkv, int D, int64_t num_slots,
+                             void* stream) {
+    if (n_tokens < 0 || Hkv < 1 || D < 8 || D % 8 || num_slots < 1) return D3D_E_SHAPE;
+    if (n_tokens == 0) return D3D_OK;
+    if (!k || !v || !k_cache || !v_cache || !slot_mapping) return D3D_E_NULL;
+    hipLaunchKernelGGL(attn::kv_append_kernel, dim3(n_tokens), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+                       static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), slot_mapping, Hkv * D,
+                       num_slots);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}

@@ -94,6 +94,63 @@ int d3d_accept_fused(const void* target, const void* draft, int dtype, int input
                      uint8_t* all_accepted, int64_t* posterior, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/*
+ * Bytes of workspace the paged attention entry points need (split-context
+ * partials).  max_context bounds every context_lens[b]; the same value must
+ * be passed to the attention call.
+ */
+size_t d3d_attn_workspace_bytes(int B, int Q, int Hq, int Hkv, int D, int page_size,
+                                int max_context);
+
+/*
+ * Block-verify attention over a paged KV cache, causal within the block.
+ *
+ * Replaces flash_attn_with_kvcache(q, k_cache, v_cache, cache_seqlens,
+ * block_table, causal=True, softmax_scale) at
+ * serving/vendor/ssd/layers/attention.py:38-41.
+ *
+ * q, out       [B, Q, Hq, D] bf16
+ * k_cache, v_cache [num_pages, page_size, Hkv, D] bf16 (layout of
+ *              serving/backend.py:46-48)
+ * block_table  [B, max_pages] int32 page ids
+ * context_lens [B] int32, keys per request including the block's own Q
+ *              keys (already appended); query i sees keys
+ *              j <= context_lens[b] - Q + i
+ * D must be 128; (Hq / Hkv) * Q <= 128.  Page ids outside [0, num_pages)
+ * read as zero keys/values instead of faulting.
+ */
+int d3d_verify_attn_paged(const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_table, const int32_t* context_lens, void* out,
+                          int B, int Q, int Hq, int Hkv, int D, int page_size, int max_pages,
+                          int num_pages, float scale, int max_context, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * Diffusion-draft block attention: as d3d_verify_attn_paged, but every
+ * query of the block sees every key j < context_lens[b] (prefix plus the
+ * bidirectional block).
+ *
+ * Replaces the draft branch of serving/vendor/ssd/layers/attention.py:42-52
+ * under the recovery mask of serving/engine.py:41-42 (cols < prefix + Q), and
+ * the all-true block mask of the single-request draft step
+ * (single/eval_sync.py:531-540 with models/d3d/modeling_d3d.py:345-364).
+ */
+int d3d_draft_block_attn(const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* block_table, const int32_t* context_lens, void* out,
+                         int B, int Q, int Hq, int Hkv, int D, int page_size, int max_pages,
+                         int num_pages, float scale, int max_context, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
+ * KV append: k_cache.view(-1, Hkv, D)[slot_mapping] = k (and v), as at
+ * serving/vendor/ssd/layers/attention.py:21-22.  k, v [n_tokens, Hkv, D]
+ * bf16; slot_mapping [n_tokens] int64; num_slots = num_pages * page_size.
+ * Slots outside [0, num_slots) are skipped.
+ */
+int d3d_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
+                  const int64_t* slot_mapping, int n_tokens, int Hkv, int D, int64_t num_slots,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

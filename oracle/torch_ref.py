@@ -9,6 +9,11 @@ fp32 torch-CPU restatement of the reference acceptance path, op for op:
                          inverse CDF ``first t with cumsum(dist)_t > v*sum``
 * ``verify_block_sparse`` single/speculative_sampling.py:79-143, same changes
 * ``greedy``             single/eval_sync.py:1223-1234
+* ``paged_attention_sdpa`` the reference's draft-branch pattern
+                         (serving/vendor/ssd/layers/attention.py:42-52):
+                         gather pages, repeat_interleave the KV heads, SDPA
+                         with an explicit mask -- in fp32, with the causal
+                         block mask of flash_attn_with_kvcache for verify
 
 It rounds the way the reference's own tensor ops round on CPU, so together
 with the fp64 C oracle it brackets the kernel's fp32 results.  It also is the
@@ -98,3 +103,26 @@ def greedy(target_logits: torch.Tensor, block: torch.Tensor):
     accepted_tail = matches.long().cumprod(dim=1).sum(dim=1)
     correction = posterior.gather(1, accepted_tail[:, None])[:, 0]
     return accepted_tail, correction, posterior
+
+
+def paged_attention_sdpa(q, k_cache, v_cache, block_table, context_lens, scale, causal=True):
+    """fp32 torch-CPU paged attention; q [B,Q,Hq,D], caches [P,ps,Hkv,D]."""
+    B, Q, Hq, D = q.shape
+    P, ps, Hkv, _ = k_cache.shape
+    outs = []
+    for b in range(B):
+        ctx = int(context_lens[b])
+        t = torch.arange(ctx)
+        slots = block_table[b].long()[t // ps] * ps + t % ps
+        keys = k_cache.reshape(-1, Hkv, D)[slots].float().transpose(0, 1)
+        vals = v_cache.reshape(-1, Hkv, D)[slots].float().transpose(0, 1)
+        keys = keys.repeat_interleave(Hq // Hkv, 0)
+        vals = vals.repeat_interleave(Hq // Hkv, 0)
+        queries = q[b].float().transpose(0, 1)
+        if causal:
+            mask = torch.arange(ctx)[None, :] <= (ctx - Q + torch.arange(Q))[:, None]
+        else:
+            mask = torch.ones(Q, ctx, dtype=torch.bool)
+        o = torch.nn.functional.scaled_dot_product_attention(queries, keys, vals, attn_mask=mask, scale=scale)
+        outs.append(o.transpose(0, 1))
+    return torch.stack(outs)
