@@ -39,6 +39,9 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-models", action="store_true",
+                    help="skip the draft-block (1.7B) and end-to-end (8B + 1.7B) model runs")
+    ap.add_argument("--e2e-new-tokens", type=int, default=512)
     return ap.parse_args()
 
 
@@ -136,6 +139,39 @@ def time_calls(fn, steps: int, warmup: int, dev) -> float:
     end.record(s)
     torch.cuda.synchronize(dev)
     return start.elapsed_time(end) / steps
+
+
+def draft_block_bench(dev, reps: int = 5):
+    """Diffusion-draft block step at Qwen3-1.7B draft shapes (random bf16 weights):
+    batch 4, 1024-token prefix, one block of 16 masks, 4 iterations of top-4."""
+    from d3d_amd import draft as dr
+    from d3d_amd.model import D3D_1P7B, PagedKV, Qwen3PagedModel, Sequence, prefill
+    model = Qwen3PagedModel(D3D_1P7B, dev, draft=True, seed=11)
+    kv = PagedKV(D3D_1P7B, 512, 16, dev)
+    g = torch.Generator().manual_seed(5)
+    seqs = [Sequence(i, torch.randint(0, 151936, (1024,), generator=g).tolist()) for i in range(4)]
+    prefill(model, kv, seqs, "draft")
+    block = torch.full((4, 16), dr.MASK_ID, dtype=torch.int64, device=dev)
+    dr.d3d_draft_block(model, kv, seqs, block, 4)
+    torch.cuda.synchronize(dev)
+    ms = time_calls(lambda: dr.d3d_draft_block(model, kv, seqs, block, 4), reps, 1, dev)
+    del model, kv
+    torch.cuda.empty_cache()
+    return ms
+
+
+def e2e_bench(dev, new_tokens: int):
+    """Qwen3-8B-shaped target + Qwen3-1.7B-shaped draft co-resident, two streams:
+    batch 4, prompts of 512 random ids, greedy, 16-token blocks, 16-token pages."""
+    from d3d_amd.engine import Engine
+    eng = Engine(seed=42)
+    g = torch.Generator().manual_seed(9)
+    prompts = torch.randint(0, 151936, (4, 512), generator=g).tolist()
+    eng.generate([p[:64] for p in prompts], max_new_tokens=8, ignore_eos=True)  # warm-up
+    res = eng.generate(prompts, max_new_tokens=new_tokens, ignore_eos=True)
+    del eng
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(seconds: float):
@@ -259,6 +295,20 @@ def main():
         "draft_attn_b4_us": round(dr_ms * 1e3, 2),
         "draft_attn_b4_gbps": round(dr.bytes / (dr_ms * 1e-3) / 1e9, 1),
     }
+    if not args.no_models:
+        out["draft_block_step_ms"] = round(draft_block_bench(dev), 3)
+        res = e2e_bench(dev, args.e2e_new_tokens)
+        out["e2e"] = {
+            "steps_per_s": round(res["steps_per_s"], 2),
+            "tokens_per_s": round(res["tps"], 1),
+            "verify_ms": round(res["verify_ms"], 3),
+            "draft_ms": round(res["draft_ms"], 3),
+            "overlap_fraction": round(res["overlap_fraction"], 3),
+            "steps": res["steps"],
+            "new_tokens": args.e2e_new_tokens,
+            "batch": 4,
+            "note": "random weights: drafts almost never match, so each step commits 1 token",
+        }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -33,6 +33,7 @@
 // inverse CDF over the unnormalised weights driven by resample_u:
 // token = first t with C_t > u * W, else the last t with positive weight.
 #include "d3d_common.hpp"
+#include "rowstats.hpp"
 #include "../../include/d3d_hip.h"
 
 #include <limits.h>
@@ -40,23 +41,14 @@
 namespace d3d {
 namespace accept {
 
-constexpr int NT = 256;          // threads per workgroup (4 waves)
-constexpr int kChunk = 4096;     // vocabulary entries per chunk
-constexpr int L = kChunk / NT;   // entries per thread per chunk
+using namespace rows;
+
 constexpr int kMaxK = 127;       // K+1 target rows + K draft rows <= 255
-constexpr int kMaxStatLds = 2048;  // RowStat entries staged in LDS per batch (32 KiB)
 // Phases 2 and 3 are latency-bound, so their chunks hold nv2 16-byte vectors
 // per thread (nv2 in 1..kMaxNv2), chosen per launch: few requests get fine
 // chunks (more workgroups, shorter per-thread chains), many requests get
 // coarse ones (fewer redundant row merges).
 constexpr int kMaxNv2 = 4;
-
-struct RowStat {
-    float m;     // max of z over the chunk (logits), 0 (probs)
-    float s;     // sum exp(z - m) (logits) or sum x (probs)
-    float xmax;  // max raw value
-    int arg;     // first index of xmax
-};
 
 struct Decision {
     int n;  // first rejected position (K when all accepted)
@@ -73,8 +65,6 @@ struct ResStat {
 };
 
 enum : int { kFlagInvalid = 1 };
-
-enum Mode : int { kGreedy = 0, kLogits = 1, kProbs = 2 };
 
 struct Params {
     const void* target;
@@ -99,220 +89,7 @@ struct Params {
     int64_t* posterior;
 };
 
-template <int DT>
-struct Vec;
-template <>
-struct Vec<kF32> {
-    static constexpr int E = 4;
-    static constexpr size_t bytes = 4;
-};
-template <>
-struct Vec<kBF16> {
-    static constexpr int E = 8;
-    static constexpr size_t bytes = 2;
-};
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <int DT>
-__device__ __forceinline__ const void* row_ptr(const void* base, size_t row, int V) {
-    return static_cast<const char*>(base) + row * (size_t)V * Vec<DT>::bytes;
-}
-
-template <int DT>
-__device__ __forceinline__ float load_one(const void* row, int e) {
-    if constexpr (DT == kF32) {
-        return static_cast<const float*>(row)[e];
-    } else {
-        return bf16_bits_to_f32(static_cast<const uint16_t*>(row)[e]);
-    }
-}
-
-// Loads L entries of one row into x[]: x[j*E + k] holds entry
-// first + j*stride + k.  Entries at or beyond V read as FILL (-inf for logits,
-// 0 for probabilities), which leaves every reduction unchanged, so the
-// arithmetic loops carry no bounds checks.  STREAM marks a single-use read
-// (non-temporal hint).
-template <int DT, bool VEC, bool STREAM, int LT>
-__device__ __forceinline__ void load_tile(const void* row, int V, int first, int stride, float fill,
-                                          float (&x)[LT]) {
-    constexpr int E = Vec<DT>::E;
-#pragma unroll
-    for (int j = 0; j < LT / E; ++j) {
-        const int e0 = first + j * stride;
-        if (VEC && e0 + E <= V) {
-            if constexpr (DT == kF32) {
-                const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + e0);
-                const f32x4 v = STREAM ? __builtin_nontemporal_load(p) : *p;
-                x[j * E + 0] = v.x;
-                x[j * E + 1] = v.y;
-                x[j * E + 2] = v.z;
-                x[j * E + 3] = v.w;
-            } else {
-                const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + e0);
-                const u32x4 v = STREAM ? __builtin_nontemporal_load(p) : *p;
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    x[j * E + 2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
-                    x[j * E + 2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < E; ++k) {
-                const int e = e0 + k;
-                x[j * E + k] = e < V ? load_one<DT>(row, e) : fill;
-            }
-        }
-    }
-}
-
-// As load_tile, for the first nv (runtime, <= LT/E) vectors only.
-template <int DT, bool VEC, int LT>
-__device__ __forceinline__ void load_tile_n(const void* row, int V, int first, int stride, int nv, float fill,
-                                            float (&x)[LT]) {
-    constexpr int E = Vec<DT>::E;
-#pragma unroll
-    for (int j = 0; j < LT / E; ++j) {
-        if (j >= nv) break;
-        const int e0 = first + j * stride;
-        if (VEC && e0 + E <= V) {
-            if constexpr (DT == kF32) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + e0);
-                x[j * E + 0] = v.x;
-                x[j * E + 1] = v.y;
-                x[j * E + 2] = v.z;
-                x[j * E + 3] = v.w;
-            } else {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + e0);
-                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    x[j * E + 2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
-                    x[j * E + 2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < E; ++k) {
-                const int e = e0 + k;
-                x[j * E + k] = e < V ? load_one<DT>(row, e) : fill;
-            }
-        }
-    }
-}
-
-template <int DT>
-__device__ __forceinline__ int tile_index(int first, int stride, int l) {
-    constexpr int E = Vec<DT>::E;
-    return first + (l / E) * stride + (l % E);
-}
-
-template <Mode M>
-__device__ __forceinline__ constexpr float fill_value() {
-    return M == kProbs ? 0.f : -INFINITY;
-}
-
-// Probability of one entry given its row statistics: softmax(x / T) entry
-// exp(x / T - M) / S for logits, x / max(S, 1e-12) for probabilities.
-// inv_s is 1 / S (logits) or 1 / max(S, 1e-12) (probabilities).
-template <Mode M, bool UNIT_T>
-__device__ __forceinline__ float prob_of(float x, float rowM, float inv_s, float T) {
-    if constexpr (M == kProbs) {
-        return x * inv_s;
-    } else {
-        return expf((UNIT_T ? x : x / T) - rowM) * inv_s;
-    }
-}
-
-template <Mode M>
-__device__ __forceinline__ float inv_sum(float S) {
-    return M == kProbs ? 1.0f / fmaxf(S, 1e-12f) : 1.0f / S;
-}
-
-__device__ __forceinline__ int wave_max_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-__device__ __forceinline__ int wave_min_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-__device__ __forceinline__ int block_max_int(int v, int* scratch) {
-    v = wave_max_int(v);
-    __syncthreads();
-    if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
-    __syncthreads();
-    int r = scratch[0];
-#pragma unroll
-    for (int k = 1; k < NT / kWave; ++k) r = max(r, scratch[k]);
-    return r;
-}
-
-__device__ __forceinline__ int block_min_int(int v, int* scratch) {
-    v = wave_min_int(v);
-    __syncthreads();
-    if ((threadIdx.x & (kWave - 1)) == 0) scratch[threadIdx.x / kWave] = v;
-    __syncthreads();
-    int r = scratch[0];
-#pragma unroll
-    for (int k = 1; k < NT / kWave; ++k) r = min(r, scratch[k]);
-    return r;
-}
-
 // ---------------------------------------------------------------- phase 1
-template <int DT, Mode M, bool UNIT_T>
-__device__ __forceinline__ RowStat chunk_stats(const float (&x)[L], int first, float T, bool want_arg,
-                                               float* rf, int* ri) {
-    constexpr int E = Vec<DT>::E;
-    float bv = x[0];
-    int bi = first;
-    if (want_arg) {
-        // Entries are visited in increasing index order, so ">" keeps the first max.
-#pragma unroll
-        for (int l = 1; l < L; ++l) {
-            if (x[l] > bv) {
-                bv = x[l];
-                bi = tile_index<DT>(first, NT * E, l);
-            }
-        }
-        block_argmax<NT>(bv, bi, rf, ri);
-    } else {
-#pragma unroll
-        for (int l = 1; l < L; ++l) bv = fmaxf(bv, x[l]);
-        bv = block_max<NT>(bv, rf);
-        bi = INT_MAX;
-    }
-    RowStat st;
-    st.xmax = bv;
-    st.arg = bi;
-    st.m = 0.f;
-    st.s = 0.f;
-    if constexpr (M == kProbs) {
-        float s = 0.f;
-#pragma unroll
-        for (int l = 0; l < L; ++l) s += x[l];
-        st.s = block_sum<NT>(s, rf);
-    } else if constexpr (M == kLogits) {
-        // max z equals (max x) / T: division by T > 0 is monotone.
-        const float m = UNIT_T ? bv : bv / T;
-        float s = 0.f;
-        if (m != -INFINITY) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) s += expf((UNIT_T ? x[l] : x[l] / T) - m);
-        }
-        st.m = m;
-        st.s = block_sum<NT>(s, rf);
-    }
-    return st;
-}
-
 template <int DT, bool VEC, Mode M>
 __global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
     constexpr int E = Vec<DT>::E;
@@ -342,67 +119,13 @@ __global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
 }
 
 // ---------------------------------------------------------------- phase 2
-constexpr int kLanesPerRow = 8;
-constexpr int kRowsPerPass = NT / kLanesPerRow;
-
 // Row statistics of request b: sM/sS per row (target rows 0..K, draft rows
-// K+1..2K) and sArg for target rows.  Chunk records are staged in LDS; 8
-// lanes per row then take every 8th chunk: first the row max (and argmax) by
-// a fold and a 3-step butterfly, then sum_c s_c * exp(m_c - M) with
-// independent exponentials, folded and butterflied the same way.
+// K+1..2K) and sArg for target rows.
 template <Mode M>
 __device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, float* sS, int* sArg,
                                            RowStat* lds) {
     const int K = P.K, C = P.C, R = 2 * K + 1;
-    const int rows = M == kGreedy ? K + 1 : R;
-    const int g = threadIdx.x % kLanesPerRow;
-    const int batch_rows = min(rows, kMaxStatLds / C);  // >= 1: C <= kMaxStatLds
-    for (int r0 = 0; r0 < rows; r0 += batch_rows) {
-        const int nr = min(batch_rows, rows - r0);
-        const RowStat* src = P.stats + ((size_t)b * R + r0) * C;
-        __syncthreads();
-        for (int e = threadIdx.x; e < nr * C; e += NT) lds[e] = src[e];
-        __syncthreads();
-        for (int rr0 = 0; rr0 < nr; rr0 += kRowsPerPass) {
-            const int rr = rr0 + threadIdx.x / kLanesPerRow;
-            const bool live = rr < nr;
-            float m = -INFINITY, xm = -INFINITY;
-            int am = INT_MAX;
-            if (live) {
-                for (int k = g; k < C; k += kLanesPerRow) {
-                    const RowStat t = lds[rr * C + k];
-                    m = fmaxf(m, t.m);
-                    argmax_merge(xm, am, t.xmax, t.arg);
-                }
-            }
-#pragma unroll
-            for (int o = 1; o < kLanesPerRow; o <<= 1) {
-                m = fmaxf(m, __shfl_xor(m, o, kWave));
-                const float x2 = __shfl_xor(xm, o, kWave);
-                const int a2 = __shfl_xor(am, o, kWave);
-                argmax_merge(xm, am, x2, a2);
-            }
-            float s = 0.f;
-            if (live && M != kGreedy) {
-                for (int k = g; k < C; k += kLanesPerRow) {
-                    const RowStat t = lds[rr * C + k];
-                    if constexpr (M == kProbs) {
-                        s += t.s;
-                    } else {
-                        if (t.m != -INFINITY) s += t.s * expf(t.m - m);
-                    }
-                }
-            }
-#pragma unroll
-            for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o, kWave);
-            if (live && g == 0) {
-                sM[r0 + rr] = m;
-                sS[r0 + rr] = s;
-                if (r0 + rr <= K) sArg[r0 + rr] = am;
-            }
-        }
-    }
-    __syncthreads();
+    merge_row_stats<M>(P.stats + (size_t)b * R * C, M == kGreedy ? K + 1 : R, C, K + 1, sM, sS, sArg, lds);
 }
 
 template <int DT, bool VEC, Mode M, bool UNIT_T>
@@ -563,22 +286,6 @@ __global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
 }
 
 // ---------------------------------------------------------------- phase 3
-// Inclusive scan over the workgroup in thread order (fixed order).
-__device__ __forceinline__ float block_incl_scan(float v, float* s_wave) {
-    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const float t = __shfl_up(v, o, kWave);
-        if (lane >= o) v += t;
-    }
-    __syncthreads();
-    if (lane == kWave - 1) s_wave[wv] = v;
-    __syncthreads();
-    float off = 0.f;
-    for (int k = 0; k < wv; ++k) off += s_wave[k];
-    return v + off;
-}
-
 template <int DT, bool VEC, Mode M, bool UNIT_T>
 __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_wave, float* s_f, int* s_i,
                                               int* ri) {

@@ -1,0 +1,149 @@
+// Confidence and top-k unmask for one diffusion-draft denoise iteration.
+//
+// Reference behaviour (D3D repository):
+//   single/eval_sync.py:447-465  _select_transfer: scores = confidence where
+//       the block holds MASK_ID (else -1), top-k, block[idx] = x0[idx]
+//   single/eval_sync.py:713-717  greedy confidence: x0 = argmax(logits),
+//       x0_p = max softmax(logits) probability
+//   third_party/sglang/python/sglang/srt/dllm/algorithm/low_confidence.py:32-35
+//       the same confidence for SGLang's LowConfidence
+// Differences, on purpose: selection is per request (the reference applies
+// row 0's indices to every row, eval_sync.py:461-464), and ties in confidence
+// go to the lowest position.  With temperature T > 1e-5 the confidence is the
+// argmax token's probability under softmax(logits / T); x0 stays the argmax.
+//
+// Two kernels: row statistics of every (request, position) row, streamed once
+// in 4096-entry chunks (HBM-bound), then one workgroup per request merges the
+// chunk records, computes conf = 1 / sum exp(z - max z) and x0, ranks the
+// masked positions and writes the unmasked tokens into the block in place.
+#include "d3d_common.hpp"
+#include "rowstats.hpp"
+#include "../../include/d3d_hip.h"
+
+#include <limits.h>
+
+namespace d3d {
+namespace conf {
+
+using namespace rows;
+
+constexpr int kMaxQ = 1024;  // positions per request
+
+struct Params {
+    const void* logits;  // [B, Q, V]
+    int64_t* block;      // [B, Q]
+    int64_t mask_id;
+    int k;
+    float T;
+    int Q, V, C;
+    RowStat* stats;  // [B][Q][C]
+    int64_t* x0;     // [B, Q] (may be null)
+    float* conf;     // [B, Q] (may be null)
+};
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(NT) void conf_stats_kernel(Params P) {
+    constexpr int E = Vec<DT>::E;
+    const int c = blockIdx.x, i = blockIdx.y, b = blockIdx.z;
+    __shared__ float rf[NT / kWave];
+    __shared__ int ri[NT / kWave];
+    const void* row = row_ptr<DT>(P.logits, (size_t)b * P.Q + i, P.V);
+    const int first = c * kChunk + threadIdx.x * E;
+    float x[L];
+    load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, fill_value<kLogits>(), x);
+    const RowStat st = P.T == 1.0f ? chunk_stats<DT, kLogits, true>(x, first, P.T, true, rf, ri)
+                                   : chunk_stats<DT, kLogits, false>(x, first, P.T, true, rf, ri);
+    if (threadIdx.x == 0) P.stats[((size_t)b * P.Q + i) * P.C + c] = st;
+}
+
+__global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
+    const int b = blockIdx.x;
+    const int Q = P.Q;
+    __shared__ RowStat lds[kMaxStatLds];
+    __shared__ float sM[kMaxQ], sS[kMaxQ];
+    __shared__ int sArg[kMaxQ];
+    __shared__ uint8_t sMask[kMaxQ];
+    __shared__ int s_masked;
+
+    // Block ids are loaded before the merge so the load overlaps it.
+    for (int i = threadIdx.x; i < Q; i += NT) sMask[i] = P.block[(size_t)b * Q + i] == P.mask_id;
+    if (threadIdx.x == 0) s_masked = 0;
+    merge_row_stats<kLogits>(P.stats + (size_t)b * Q * P.C, Q, P.C, Q, sM, sS, sArg, lds);
+    // The argmax entry's probability is exp(z_max - M) / S = 1 / S.
+    for (int i = threadIdx.x; i < Q; i += NT) {
+        const float cf = 1.0f / sS[i];
+        sS[i] = cf;
+        if (P.conf) P.conf[(size_t)b * Q + i] = cf;
+        if (P.x0) P.x0[(size_t)b * Q + i] = sArg[i];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int i = 0; i < Q; ++i) n += sMask[i];
+        s_masked = n;
+    }
+    __syncthreads();
+    const int kk = min(P.k, s_masked);
+    // Rank of a masked position among masked positions: higher confidence
+    // first, then lower index.
+    for (int i = threadIdx.x; i < Q; i += NT) {
+        if (!sMask[i]) continue;
+        const float ci = sS[i];
+        int rank = 0;
+        for (int j = 0; j < Q; ++j)
+            if (sMask[j] && (sS[j] > ci || (sS[j] == ci && j < i))) ++rank;
+        if (rank < kk) P.block[(size_t)b * Q + i] = sArg[i];
+    }
+}
+
+template <int DT, bool VEC>
+static hipError_t launch(const Params& P, int B, hipStream_t s) {
+    hipLaunchKernelGGL((conf_stats_kernel<DT, VEC>), dim3(P.C, P.Q, B), dim3(NT), 0, s, P);
+    hipLaunchKernelGGL(conf_select_kernel, dim3(B), dim3(NT), 0, s, P);
+    return hipGetLastError();
+}
+
+static int num_chunks(int64_t V) { return (int)((V + kChunk - 1) / kChunk); }
+
+}  // namespace conf
+}  // namespace d3d
+
+using namespace d3d;
+
+extern "C" size_t d3d_confidence_workspace_bytes(int B, int Q, int64_t V) {
+    if (B < 1 || Q < 1 || V < 1) return 0;
+    return ((size_t)B * Q * conf::num_chunks(V) * sizeof(rows::RowStat) + 255) & ~(size_t)255;
+}
+
+extern "C" int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids, int64_t mask_id,
+                                          int k, float temperature, int B, int Q, int64_t V, int64_t* x0_out,
+                                          float* conf_out, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
+    using namespace conf;
+    if (B < 1 || B > 65535 || Q < 1 || Q > kMaxQ || V < 1 || V > (int64_t)kMaxStatLds * kChunk || k < 0)
+        return D3D_E_SHAPE;
+    if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
+    if (!logits || !block_ids || !workspace) return D3D_E_NULL;
+    if (workspace_bytes < d3d_confidence_workspace_bytes(B, Q, V)) return D3D_E_WORKSPACE;
+    Params P;
+    P.logits = logits;
+    P.block = block_ids;
+    P.mask_id = mask_id;
+    P.k = k;
+    P.T = temperature > 1e-5f ? temperature : 1.0f;
+    P.Q = Q;
+    P.V = (int)V;
+    P.C = num_chunks(V);
+    P.stats = static_cast<rows::RowStat*>(workspace);
+    P.x0 = x0_out;
+    P.conf = conf_out;
+    const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;
+    const bool vec = ((uintptr_t)logits % 16 == 0) && ((size_t)V * esize) % 16 == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (dtype == D3D_DTYPE_F32)
+        err = vec ? launch<kF32, true>(P, B, s) : launch<kF32, false>(P, B, s);
+    else
+        err = vec ? launch<kBF16, true>(P, B, s) : launch<kBF16, false>(P, B, s);
+    return err == hipSuccess ? D3D_OK : (int)err;
+}

@@ -1,0 +1,241 @@
+"""Qwen3-shaped paged models for the verify (target) and draft forwards.
+
+Host code in PyTorch-ROCm (GEMMs on hipBLASLt); attention, KV append and
+the speculative reductions run on the gfx950 kernels.  Weights are
+random-initialised bf16 (there are no checkpoints on this path's benchmarks).
+
+Reference structure followed:
+
+* target -- serving/vendor/ssd/models/qwen3.py:14-325: fused QKV and
+  gate-up projections, per-head q/k RMSNorm (RMSHeadNorm), rotary
+  embedding computed in fp32 from a cos/sin cache
+  (serving/vendor/ssd/layers/rotary_embedding.py:6-16, :19-60), fused
+  residual add + RMSNorm (serving/vendor/ssd/layers/layernorm.py:53-98),
+  SiLU-and-mul MLP, untied LM head;
+* draft -- models/d3d/modeling_d3d.py: the same backbone with q/k RMSNorm
+  and HF-style RoPE whose cos/sin are cast to the activation dtype
+  (:164-187, :470-516), attention through the paged draft branch
+  (serving/d3d_adapter.py:20-51).
+
+Block attention: the target attends causally within the 16-token block
+(flash_attn_with_kvcache, serving/vendor/ssd/layers/attention.py:38-41); the
+draft block sees the prefix and the whole block (recovery mask,
+serving/engine.py:41-42).  Prompt prefill reuses the block kernel: slice j of
+16 prompt tokens is run as its own request with context 16 (j + 1), which is
+exactly causal attention over the prompt.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+
+from . import attention as att
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    mlp: int
+    vocab: int = 151936
+    rope_theta: float = 1_000_000.0
+    eps: float = 1e-6
+
+    @property
+    def params(self) -> int:
+        h, d = self.hidden, self.head_dim
+        per_layer = (h * (self.heads + 2 * self.kv_heads) * d + self.heads * d * h + 3 * h * self.mlp
+                     + 2 * h + 2 * d)
+        return 2 * self.vocab * h + self.layers * per_layer + h
+
+
+# Qwen3-8B-shaped target and Qwen3-1.7B-shaped D3D draft (2,031,739,904
+# parameters with an untied LM head).
+QWEN3_8B = ModelShape(layers=36, hidden=4096, heads=32, kv_heads=8, head_dim=128, mlp=12288)
+D3D_1P7B = ModelShape(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, mlp=6144)
+
+
+class PagePool:
+    """Page allocator over a fixed pool (serving/vendor/ssd/engine/block_manager.py:65-88)."""
+
+    def __init__(self, num_pages: int):
+        self.num_pages = num_pages
+        self.free: List[int] = list(range(num_pages))
+
+    def alloc(self, n: int) -> List[int]:
+        if n > len(self.free):
+            raise RuntimeError(f"page pool exhausted: need {n}, have {len(self.free)}")
+        out, self.free = self.free[:n], self.free[n:]
+        return out
+
+    def release(self, pages: Sequence[int]) -> None:
+        self.free.extend(pages)
+
+
+class PagedKV:
+    """Per-layer K/V caches [num_pages, page_size, Hkv, D] bf16 (serving/backend.py:46-48)."""
+
+    def __init__(self, shape: ModelShape, num_pages: int, page_size: int, device):
+        self.page_size = page_size
+        self.num_pages = num_pages
+        self.k = [torch.zeros(num_pages, page_size, shape.kv_heads, shape.head_dim, dtype=torch.bfloat16,
+                              device=device) for _ in range(shape.layers)]
+        self.v = [torch.zeros_like(t) for t in self.k]
+        self.pool = PagePool(num_pages)
+
+
+class Qwen3PagedModel(torch.nn.Module):
+    """Random-initialised bf16 Qwen3-shaped model over a paged KV cache."""
+
+    def __init__(self, shape: ModelShape, device, *, draft: bool, seed: int = 0, init_std: float = 0.02):
+        super().__init__()
+        self.shape, self.draft, self.device = shape, draft, torch.device(device)
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        h, d, Hq, Hkv = shape.hidden, shape.head_dim, shape.heads, shape.kv_heads
+
+        def w(*dims):
+            return (torch.randn(*dims, generator=g, device=self.device) * init_std).to(torch.bfloat16)
+
+        def ones(n):
+            return torch.ones(n, dtype=torch.bfloat16, device=self.device)
+
+        self.embed = w(shape.vocab, h)
+        self.layers = []
+        for _ in range(shape.layers):
+            self.layers.append(dict(
+                qkv=w((Hq + 2 * Hkv) * d, h), o=w(h, Hq * d), gate_up=w(2 * shape.mlp, h),
+                down=w(h, shape.mlp), ln1=ones(h), ln2=ones(h), qn=ones(d), kn=ones(d)))
+        self.norm = ones(h)
+        self.lm_head = w(shape.vocab, h)
+        half = d // 2
+        self.inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, half, device=self.device,
+                                                                   dtype=torch.float32) * 2 / d))
+
+    # -- layers ---------------------------------------------------------------
+    def _rms(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.shape.eps)
+        return xf.to(x.dtype) * weight
+
+    def _rope(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """x [T, H, D]; positions [T]."""
+        freqs = positions.float()[:, None] * self.inv_freq[None, :]
+        cos, sin = freqs.cos()[:, None, :], freqs.sin()[:, None, :]
+        if self.draft:
+            # HF apply_rotary_pos_emb with cos/sin cast to the activation dtype.
+            cos2 = torch.cat([cos, cos], -1).to(x.dtype)
+            sin2 = torch.cat([sin, sin], -1).to(x.dtype)
+            x1, x2 = x.chunk(2, dim=-1)
+            return x * cos2 + torch.cat([-x2, x1], -1) * sin2
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1).to(x.dtype)
+
+    def forward(self, ids: torch.Tensor, positions: torch.Tensor, kv: PagedKV, block_tables: torch.Tensor,
+                context_lens: torch.Tensor, slot_mapping: torch.Tensor, *, causal: bool,
+                max_context: int) -> torch.Tensor:
+        """Hidden states [B, Q, hidden] of a block of Q tokens per request.
+
+        The block's K/V are appended at ``slot_mapping`` before attention;
+        ``context_lens`` counts the prefix plus the block.
+        """
+        B, Q = ids.shape
+        s = self.shape
+        Hq, Hkv, d = s.heads, s.kv_heads, s.head_dim
+        pos = positions.reshape(-1)
+        x = F.embedding(ids.reshape(-1), self.embed)
+        residual = None
+        for li, L in enumerate(self.layers):
+            if residual is None:
+                residual = x
+            else:
+                residual = residual + x
+            hs = self._rms(residual, L["ln1"])
+            qkv = F.linear(hs, L["qkv"])
+            q, k, v = qkv.split([Hq * d, Hkv * d, Hkv * d], dim=-1)
+            q = self._rope(self._rms(q.reshape(-1, Hq, d), L["qn"]), pos)
+            k = self._rope(self._rms(k.reshape(-1, Hkv, d), L["kn"]), pos)
+            att.kv_append(k, v.reshape(-1, Hkv, d), kv.k[li], kv.v[li], slot_mapping)
+            o = att.flash_attn_with_kvcache(q.reshape(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens,
+                                            block_tables, causal=causal, max_seqlen_k=max_context)
+            x = F.linear(o.reshape(B * Q, Hq * d), L["o"])
+            residual = residual + x
+            hs = self._rms(residual, L["ln2"])
+            gu = F.linear(hs, L["gate_up"])
+            gate, up = gu.chunk(2, dim=-1)
+            x = F.linear(F.silu(gate) * up, L["down"])
+        out = self._rms(residual + x, self.norm)
+        return out.reshape(B, Q, s.hidden)
+
+    def logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        return F.linear(hidden, self.lm_head)
+
+
+# -- page bookkeeping (serving/backend.py:55-76, :123-124) --------------------
+class Sequence:
+    """One request: token ids, committed prefix length and its page table."""
+
+    def __init__(self, seq_id: int, token_ids: List[int]):
+        self.seq_id = seq_id
+        self.token_ids = list(token_ids)
+        self.prefix = len(token_ids)
+        self.pages: dict = {}  # model name -> list of page ids
+
+
+def reserve(kv: PagedKV, seq: Sequence, name: str, length: int) -> None:
+    table = seq.pages.setdefault(name, [])
+    missing = -(-length // kv.page_size) - len(table)
+    if missing > 0:
+        table.extend(kv.pool.alloc(missing))
+
+
+def trim(kv: PagedKV, seq: Sequence, name: str, length: int) -> None:
+    table = seq.pages.setdefault(name, [])
+    keep = -(-length // kv.page_size)
+    if len(table) > keep:
+        kv.pool.release(table[keep:])
+        del table[keep:]
+
+
+def release(kv: PagedKV, seq: Sequence, name: str) -> None:
+    kv.pool.release(seq.pages.pop(name, []))
+
+
+def block_inputs(kv: PagedKV, seqs: Sequence, name: str, starts: List[int], Q: int, device):
+    """Page tables, slots and context lengths for a block of Q tokens at starts[b]."""
+    width = max(len(s.pages[name]) for s in seqs)
+    tables = torch.tensor([s.pages[name] + [0] * (width - len(s.pages[name])) for s in seqs],
+                          dtype=torch.int32)
+    st = torch.tensor(starts, dtype=torch.int64)
+    logical = st[:, None] + torch.arange(Q)[None, :]
+    slots = tables.long().gather(1, logical // kv.page_size) * kv.page_size + logical % kv.page_size
+    lens = (st + Q).to(torch.int32)
+    return (tables.to(device, non_blocking=True), slots.reshape(-1).to(device, non_blocking=True),
+            lens.to(device, non_blocking=True), logical.to(device, non_blocking=True), int(max(starts)) + Q)
+
+
+def prefill(model: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], name: str, block: int = 16) -> torch.Tensor:
+    """Writes the prompts' K/V and returns the last prompt position's hidden state [B, hidden].
+
+    Prompt lengths must be equal multiples of ``block``: slice j of each
+    prompt runs as a request with context block * (j + 1) (causal prefill).
+    """
+    dev = model.device
+    n = len(seqs[0].token_ids)
+    if any(len(s.token_ids) != n for s in seqs) or n % block:
+        raise ValueError("prefill expects equal prompt lengths that are multiples of the block size")
+    for s in seqs:
+        reserve(kv, s, name, n)
+    J = n // block
+    ids = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64).reshape(len(seqs) * J, block)
+    rows = [s for s in seqs for _ in range(J)]
+    starts = [j * block for _ in seqs for j in range(J)]
+    tables, slots, lens, logical, max_ctx = block_inputs(kv, rows, name, starts, block, dev)
+    hidden = model(ids.to(dev), logical, kv, tables, lens, slots, causal=True, max_context=max_ctx)
+    return hidden.reshape(len(seqs), n, -1)[:, -1]

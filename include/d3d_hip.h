@@ -151,6 +151,28 @@ int d3d_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,
                   const int64_t* slot_mapping, int n_tokens, int Hkv, int D, int64_t num_slots,
                   void* stream);
 
+/* Bytes of workspace d3d_confidence_topk_unmask needs. */
+size_t d3d_confidence_workspace_bytes(int B, int Q, int64_t V);
+
+/*
+ * One denoise iteration of the diffusion draft: greedy token and confidence
+ * for every position, then top-k unmask of the masked positions, in place.
+ *
+ * Replaces single/eval_sync.py:447-465 (_select_transfer, low-confidence
+ * remasking) with the greedy confidence of single/eval_sync.py:713-717:
+ * x0 = argmax(logits), conf = softmax(logits / T')[x0] with T' = T when
+ * T > 1e-5, else 1.  Among positions with block_ids == mask_id the k highest
+ * confidences (ties: lowest position; all of them when k >= their count)
+ * take x0.  Selection is per request.
+ *
+ * logits [B, Q, V] fp32 or bf16; block_ids [B, Q] int64 (in/out);
+ * x0_out [B, Q] int64 and conf_out [B, Q] fp32 may be NULL.  Q <= 1024.
+ */
+int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids, int64_t mask_id,
+                               int k, float temperature, int B, int Q, int64_t V, int64_t* x0_out,
+                               float* conf_out, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,52 @@
+"""End-to-end greedy speculative loop (GPU).
+
+Greedy speculative decoding is lossless: whatever the draft proposes, each
+committed token is the target's greedy token given the tokens before it.
+The check feeds the engine's own output to the fp32 CPU restatement of the
+target (teacher forcing) and requires every token to be the restatement's
+argmax wherever its top-2 logit margin exceeds 5 % of the logit standard
+deviation (closer margins are near ties that bf16 rounding may decide
+either way); at least half of the positions must be decisive.
+"""
+from __future__ import annotations
+
+import torch
+import pytest
+
+from d3d_amd.engine import Engine
+from d3d_amd.model import ModelShape
+from oracle import model_ref
+
+pytestmark = pytest.mark.gpu
+
+TARGET = ModelShape(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=128, mlp=512, vocab=1000)
+DRAFT = ModelShape(layers=1, hidden=256, heads=4, kv_heads=2, head_dim=128, mlp=256, vocab=1000)
+
+
+def test_engine_output_is_target_greedy_decoding():
+    eng = Engine(TARGET, DRAFT, pages=256, seed=7, mask_id=999)
+    for m in (eng.target, eng.draft):
+        m.lm_head.mul_(20.0)  # logits with std ~6: top-2 margins far above rounding
+    g = torch.Generator().manual_seed(3)
+    prompts = torch.randint(0, 999, (2, 32), generator=g).tolist()
+    new = 40
+    res = eng.generate(prompts, max_new_tokens=new, ignore_eos=True)
+    assert [len(o["tokens"]) for o in res["outputs"]] == [new, new]
+    assert res["steps"] >= 1 and 0.0 <= res["overlap_fraction"] <= 1.0
+    W = model_ref.weights_fp32(eng.target)
+    for o, p in zip(res["outputs"], prompts):
+        ids = list(p)
+        decisive = 0
+        for t in o["tokens"]:
+            T = len(ids)
+            logits = model_ref.forward(W, TARGET, torch.tensor(ids), torch.arange(T),
+                                       torch.ones(T, T).tril().bool())[-1]
+            top2 = logits.topk(2).values
+            if float(top2[0] - top2[1]) > 0.05 * float(logits.std()):
+                assert t == int(logits.argmax()), f"token {T - len(p)} differs from greedy decoding"
+                decisive += 1
+            ids.append(t)  # teacher forcing with the engine's own tokens
+        assert decisive >= new // 2
+    # Engine._accepted keeps the reference's list semantics.
+    assert Engine._accepted([[5, 1, 2, 9]], [[1, 2, 7, 8]]) == [(3, 7)]
+    assert Engine._accepted([[5, 1, 2]], [[1, 2, 4]]) == [(3, 4)]
