@@ -141,7 +141,7 @@ def time_calls(fn, steps: int, warmup: int, dev) -> float:
     return start.elapsed_time(end) / steps
 
 
-def draft_block_bench(dev, reps: int = 5):
+def draft_block_bench(dev, reps: int = 20):
     """Diffusion-draft block step at Qwen3-1.7B draft shapes (random bf16 weights):
     batch 4, 1024-token prefix, one block of 16 masks, 4 iterations of top-4."""
     from d3d_amd import draft as dr
@@ -152,9 +152,10 @@ def draft_block_bench(dev, reps: int = 5):
     seqs = [Sequence(i, torch.randint(0, 151936, (1024,), generator=g).tolist()) for i in range(4)]
     prefill(model, kv, seqs, "draft")
     block = torch.full((4, 16), dr.MASK_ID, dtype=torch.int64, device=dev)
-    dr.d3d_draft_block(model, kv, seqs, block, 4)
+    graphs = {}  # each (forward + unmask) iteration replayed from a HIP graph
+    dr.d3d_draft_block(model, kv, seqs, block, 4, graphs=graphs)
     torch.cuda.synchronize(dev)
-    ms = time_calls(lambda: dr.d3d_draft_block(model, kv, seqs, block, 4), reps, 1, dev)
+    ms = time_calls(lambda: dr.d3d_draft_block(model, kv, seqs, block, 4, graphs=graphs), reps, 1, dev)
     del model, kv
     torch.cuda.empty_cache()
     return ms

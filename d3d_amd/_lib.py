@@ -112,6 +112,26 @@ def stream_ptr(device: torch.device) -> int:
 
 
 _workspaces: dict = {}
+_capture_owner: Optional[list] = None
+
+
+class capture_workspaces:
+    """Context for HIP graph capture: workspaces requested inside it are
+    allocated afresh and appended to ``owner``, which must live as long as the
+    captured graph (the graph's kernels keep their addresses)."""
+
+    def __init__(self, owner: list):
+        self.owner = owner
+
+    def __enter__(self):
+        global _capture_owner
+        self.prev, _capture_owner = _capture_owner, self.owner
+        return self.owner
+
+    def __exit__(self, *exc):
+        global _capture_owner
+        _capture_owner = self.prev
+        return False
 
 
 def workspace(device: torch.device, key: str, nbytes: int) -> torch.Tensor:
@@ -119,7 +139,16 @@ def workspace(device: torch.device, key: str, nbytes: int) -> torch.Tensor:
 
     One workspace per stream keeps calls on concurrent streams from sharing
     scratch memory; calls on one stream are ordered, so reuse is safe.
+    During a graph capture the cache is bypassed: every captured graph gets
+    its own workspace, owned by the capture_workspaces owner list.
     """
+    if torch.cuda.is_current_stream_capturing():
+        if _capture_owner is None:
+            raise RuntimeError("d3d_amd kernels captured into a graph need a workspace owner "
+                               "(wrap the capture in d3d_amd._lib.capture_workspaces)")
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _capture_owner.append(ws)
+        return ws
     sp = stream_ptr(device)
     k = (device.index, sp, key)
     ws = _workspaces.get(k)

@@ -21,7 +21,7 @@ from typing import List, Optional, Tuple
 import torch
 
 from . import _lib
-from .model import PagedKV, Qwen3PagedModel, Sequence, block_inputs, reserve
+from .model import BlockStep, PagedKV, Qwen3PagedModel, Sequence, block_inputs, reserve
 
 MASK_ID = 151669
 
@@ -74,7 +74,7 @@ def draft_block_forward(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequen
 
 def d3d_draft_block(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], block: torch.Tensor,
                     denoising_steps: int, *, mask_id: int = MASK_ID, temperature: float = 0.0,
-                    name: str = "draft") -> torch.Tensor:
+                    name: str = "draft", graphs: Optional[dict] = None, width: Optional[int] = None) -> torch.Tensor:
     """Denoise a block [B, Q] whose masked positions hold ``mask_id``.
 
     single/eval_sync.py:482-592 with greedy low-confidence remasking: each
@@ -82,16 +82,35 @@ def d3d_draft_block(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence],
     most confident masked positions; the last step fills every remaining
     mask.  ``num_masks`` is taken from request 0, as the reference's
     schedule is (:503-508).
+
+    With a ``graphs`` dict each (forward + unmask) step is replayed from a
+    HIP graph cached there per (B, Q, k, table width); ``width`` fixes the
+    page-table width (default: the current longest table).
     """
     cur = block.clone().contiguous()
     num_masks = int((cur[0] == mask_id).sum().item())
     if num_masks == 0:
         return cur
     schedule = get_num_transfer_tokens(num_masks, denoising_steps)
-    Q = cur.shape[1]
+    B, Q = cur.shape
+    starts = [s.prefix for s in seqs]
+    for s in seqs:
+        reserve(kv, s, name, s.prefix + Q)
+    tables, slots, lens, logical, _ = block_inputs(kv, seqs, name, starts, Q, drafter.device, width)
+    W = tables.shape[1]
     for step, k in enumerate(schedule):
-        logits = draft_block_forward(drafter, kv, seqs, cur, name)
         if step == len(schedule) - 1:
             k = Q  # the last step unmasks everything left (:549-550)
-        confidence_topk_unmask(logits, cur, mask_id, k, temperature)
+        if graphs is None:
+            hidden = drafter(cur, logical, kv, tables, lens, slots, causal=False, max_context=W * kv.page_size)
+            confidence_topk_unmask(drafter.logits(hidden), cur, mask_id, k, temperature)
+            continue
+        key = (B, Q, k, W, temperature)
+        step_fn = graphs.get(key)
+        if step_fn is None:
+            def post(hidden, ids, k=k):
+                confidence_topk_unmask(drafter.logits(hidden), ids, mask_id, k, temperature)
+                return ids
+            step_fn = graphs[key] = BlockStep(drafter, kv, B, Q, W, causal=False, post=post)
+        cur.copy_(step_fn(cur, logical, tables, slots, lens))
     return cur

@@ -30,9 +30,9 @@ from typing import Dict, List, Sequence as Seq, Tuple
 import torch
 
 from . import speculative_sampling as ss
-from .draft import MASK_ID, confidence_topk_unmask, draft_block_forward
-from .model import (D3D_1P7B, QWEN3_8B, ModelShape, PagedKV, Qwen3PagedModel, Sequence, block_inputs, prefill,
-                    release, reserve, trim)
+from .draft import MASK_ID, confidence_topk_unmask
+from .model import (D3D_1P7B, QWEN3_8B, BlockStep, ModelShape, PagedKV, Qwen3PagedModel, Sequence, block_inputs,
+                    prefill, release, reserve, trim)
 
 EOS_IDS = (151643, 151645)
 
@@ -40,13 +40,15 @@ EOS_IDS = (151643, 151645)
 class Engine:
     def __init__(self, target_shape: ModelShape = QWEN3_8B, draft_shape: ModelShape = D3D_1P7B, *,
                  block_size: int = 16, page_size: int = 16, pages: int = 4096, device: str = "cuda:0",
-                 seed: int = 42, mask_id: int = MASK_ID):
+                 seed: int = 42, mask_id: int = MASK_ID, use_graphs: bool = True):
         if target_shape.vocab != draft_shape.vocab:
             raise ValueError("target and draft vocabularies must match")
         if not 0 <= mask_id < draft_shape.vocab:
             raise ValueError(f"mask id {mask_id} outside the draft vocabulary")
         self.K = block_size
         self.mask_id = mask_id
+        self.use_graphs = use_graphs
+        self._cache: Dict = {}
         self.device = torch.device(device)
         self.target = Qwen3PagedModel(target_shape, self.device, draft=False, seed=seed)
         self.draft = Qwen3PagedModel(draft_shape, self.device, draft=True, seed=seed + 1)
@@ -67,29 +69,52 @@ class Engine:
             out.append((accepted, p[accepted - 1]))
         return out
 
-    # -- draft steps ---------------------------------------------------------
-    def _draft_fill(self, seqs: List[Sequence], ids: torch.Tensor, starts: List[int]) -> torch.Tensor:
-        """One draft forward of a block; masked positions take the greedy token."""
-        logits = draft_block_forward(self.draft, self.dkv, seqs, ids, "draft", starts)
-        confidence_topk_unmask(logits, ids, self.mask_id, ids.shape[1])
-        return ids
+    # -- graph-replayed block steps --------------------------------------------
+    def _steps(self, B: int, width: int):
+        """(verify, draft commit, draft fill) block steps for B requests, cached."""
+        key = (B, width)
+        if key not in self._cache:
+            K, mid = self.K, self.mask_id
 
-    def _recover(self, seqs: List[Sequence], anchors: List[int]) -> torch.Tensor:
+            def verify_post(hidden, ids):
+                out = ss.greedy_accept(self.target.logits(hidden), ids)
+                return out.accepted, out.out_token
+
+            def fill_post(hidden, ids):
+                confidence_topk_unmask(self.draft.logits(hidden), ids, mid, K)
+                return ids
+
+            self._cache[key] = (
+                BlockStep(self.target, self.tkv, B, K, width, causal=True, post=verify_post,
+                          use_graph=self.use_graphs),
+                BlockStep(self.draft, self.dkv, B, K, width, causal=True, post=None, use_graph=self.use_graphs),
+                BlockStep(self.draft, self.dkv, B, K, width, causal=False, post=fill_post,
+                          use_graph=self.use_graphs),
+            )
+        return self._cache[key]
+
+    def _fill(self, seqs: List[Sequence], ids: torch.Tensor, starts: List[int], width: int) -> torch.Tensor:
+        """One draft forward of a block; masked positions take the greedy token."""
+        for s, st in zip(seqs, starts):
+            reserve(self.dkv, s, "draft", st + self.K)
+        tables, slots, lens, logical, _ = block_inputs(self.dkv, seqs, "draft", starts, self.K, self.device, width)
+        return self._steps(len(seqs), width)[2](ids, logical, tables, slots, lens).clone()
+
+    def _recover(self, seqs: List[Sequence], anchors: List[int], width: int) -> torch.Tensor:
         """serving/engine.py:54-62: anchor + 15 masks from the committed prefix."""
         ids = torch.full((len(seqs), self.K), self.mask_id, dtype=torch.int64)
         ids[:, 0] = torch.tensor(anchors)
-        ids = ids.to(self.device, non_blocking=True)
-        return self._draft_fill(seqs, ids, [s.prefix for s in seqs])
+        return self._fill(seqs, ids.to(self.device, non_blocking=True), [s.prefix for s in seqs], width)
 
-    def _predict_full(self, seqs: List[Sequence], blocks: torch.Tensor) -> torch.Tensor:
+    def _predict_full(self, seqs: List[Sequence], blocks: torch.Tensor, width: int) -> torch.Tensor:
         """Writes the pending block's draft K/V (causal) and drafts the block after it."""
         starts = [s.prefix for s in seqs]
         for s in seqs:
             reserve(self.dkv, s, "draft", s.prefix + 2 * self.K)
-        tables, slots, lens, logical, mx = block_inputs(self.dkv, seqs, "draft", starts, self.K, self.device)
-        self.draft(blocks, logical, self.dkv, tables, lens, slots, causal=True, max_context=mx)
+        tables, slots, lens, logical, _ = block_inputs(self.dkv, seqs, "draft", starts, self.K, self.device, width)
+        self._steps(len(seqs), width)[1](blocks, logical, tables, slots, lens)
         ids = torch.full((len(seqs), self.K), self.mask_id, dtype=torch.int64, device=self.device)
-        return self._draft_fill(seqs, ids, [s.prefix + self.K for s in seqs])
+        return self._fill(seqs, ids, [s.prefix + self.K for s in seqs], width)
 
     # -- main loop -----------------------------------------------------------
     @torch.inference_mode()
@@ -104,6 +129,10 @@ class Engine:
         seqs = [Sequence(i, p) for i, p in enumerate(prompts)]
         for s in seqs:
             s.generated, s.accepts, s.hits, s.recoveries = [], [], 0, 0
+        # One page-table width for the whole run: the attention's context
+        # bound and the captured graphs stay fixed while contexts grow.
+        ps = self.tkv.page_size
+        width = -(-(max(len(p) for p in prompts) + max_new_tokens + 2 * self.K) // ps)
         origin = torch.cuda.Event(enable_timing=True)
         origin.record(torch.cuda.current_stream(dev))
         started = time.perf_counter()
@@ -117,13 +146,12 @@ class Engine:
         self.ts.synchronize()
         anchors = anchor_t.cpu().tolist()
         with torch.cuda.stream(self.ds):
-            current = self._recover(seqs, anchors)
+            current = self._recover(seqs, anchors, width)
         running = list(seqs)
         steps = 0
         verify_ms, draft_ms, overlap_ms = [], [], []
         outputs = []
         while running:
-            B = len(running)
             ev = {k: torch.cuda.Event(enable_timing=True) for k in ("vs", "ve", "ps", "pe", "rs", "re")}
             # -- target verify on ts ------------------------------------------
             self.ts.wait_stream(self.ds)
@@ -132,17 +160,16 @@ class Engine:
                 ev["vs"].record(self.ts)
                 for s in running:
                     reserve(self.tkv, s, "target", s.prefix + self.K)
-                tables, slots, lens, logical, mx = block_inputs(self.tkv, running, "target",
-                                                                [s.prefix for s in running], self.K, dev)
-                hidden = self.target(current, logical, self.tkv, tables, lens, slots, causal=True, max_context=mx)
-                out = ss.greedy_accept(self.target.logits(hidden), current)
-                res = torch.stack([out.accepted.long(), out.out_token]).to("cpu", non_blocking=True)
+                tables, slots, lens, logical, _ = block_inputs(self.tkv, running, "target",
+                                                               [s.prefix for s in running], self.K, dev, width)
+                accepted, out_token = self._steps(len(running), width)[0](current, logical, tables, slots, lens)
+                res = torch.stack([accepted.long(), out_token]).to("cpu", non_blocking=True)
                 blocks_host = current.to("cpu", non_blocking=True)
                 ev["ve"].record(self.ts)
             # -- draft prediction of the all-accepted outcome on ds -------------
             with torch.cuda.stream(self.ds):
                 ev["ps"].record(self.ds)
-                predicted = self._predict_full(running, current)
+                predicted = self._predict_full(running, current, width)
                 ev["pe"].record(self.ds)
             ev["ve"].synchronize()
             n_acc, tokens = res.tolist()
@@ -179,8 +206,10 @@ class Engine:
                     recover.append(s)
                     rec_anchor.append(anchor)
             for s in outputs:
-                release(self.tkv, s, "target")
-                release(self.dkv, s, "draft")
+                if "target" in s.pages:
+                    release(self.tkv, s, "target")
+                if "draft" in s.pages:
+                    release(self.dkv, s, "draft")
             if not remaining:
                 break
             # -- next blocks: hits reuse the prediction, misses recover ---------
@@ -193,7 +222,7 @@ class Engine:
                     nxt[dst] = predicted[src]
                     nxt[dst, 0] = torch.tensor([a for _, _, a in hit_rows], device=dev)
                 if recover:
-                    rec = self._recover(recover, rec_anchor)
+                    rec = self._recover(recover, rec_anchor, width)
                     idx = torch.tensor([remaining.index(s) for s in recover], device=dev)
                     nxt[idx] = rec
                 ev["re"].record(self.ds)
@@ -202,11 +231,11 @@ class Engine:
             ev["re"].synchronize()
             vs = origin.elapsed_time(ev["vs"])
             ve = origin.elapsed_time(ev["ve"])
-            ps = origin.elapsed_time(ev["ps"])
+            ps_ = origin.elapsed_time(ev["ps"])
             pe = origin.elapsed_time(ev["pe"])
             verify_ms.append(ve - vs)
-            draft_ms.append((pe - ps) + ev["rs"].elapsed_time(ev["re"]))
-            overlap_ms.append(max(0.0, min(ve, pe) - max(vs, ps)))
+            draft_ms.append((pe - ps_) + ev["rs"].elapsed_time(ev["re"]))
+            overlap_ms.append(max(0.0, min(ve, pe) - max(vs, ps_)))
             current = nxt
             running = remaining
         torch.cuda.synchronize(dev)

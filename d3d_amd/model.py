@@ -33,6 +33,7 @@ from typing import List, Optional, Sequence
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from . import attention as att
 
 
@@ -207,17 +208,96 @@ def release(kv: PagedKV, seq: Sequence, name: str) -> None:
     kv.pool.release(seq.pages.pop(name, []))
 
 
-def block_inputs(kv: PagedKV, seqs: Sequence, name: str, starts: List[int], Q: int, device):
-    """Page tables, slots and context lengths for a block of Q tokens at starts[b]."""
-    width = max(len(s.pages[name]) for s in seqs)
+def block_inputs(kv: PagedKV, seqs: List[Sequence], name: str, starts: List[int], Q: int, device,
+                 width: Optional[int] = None):
+    """Page tables, slots and context lengths for a block of Q tokens at starts[b].
+
+    ``width`` fixes the page-table width (and so the attention's context
+    bound, width * page_size); by default it is the longest table.
+    """
+    width = max(len(s.pages[name]) for s in seqs) if width is None else width
+    if any(len(s.pages[name]) > width for s in seqs):
+        raise ValueError("a page table is wider than the fixed width")
     tables = torch.tensor([s.pages[name] + [0] * (width - len(s.pages[name])) for s in seqs],
                           dtype=torch.int32)
     st = torch.tensor(starts, dtype=torch.int64)
     logical = st[:, None] + torch.arange(Q)[None, :]
     slots = tables.long().gather(1, logical // kv.page_size) * kv.page_size + logical % kv.page_size
     lens = (st + Q).to(torch.int32)
+    max_ctx = width * kv.page_size if width is not None else int(max(starts)) + Q
     return (tables.to(device, non_blocking=True), slots.reshape(-1).to(device, non_blocking=True),
-            lens.to(device, non_blocking=True), logical.to(device, non_blocking=True), int(max(starts)) + Q)
+            lens.to(device, non_blocking=True), logical.to(device, non_blocking=True), max_ctx)
+
+
+_WARMUP: dict = {}
+
+
+def _warmup_stream(device) -> torch.cuda.Stream:
+    """One side stream per device for pre-capture warm-ups."""
+    key = torch.device(device).index
+    if key not in _WARMUP:
+        _WARMUP[key] = torch.cuda.Stream(device)
+    return _WARMUP[key]
+
+
+class BlockStep:
+    """A block forward plus a post-processing function over static device
+    buffers, replayed from a HIP graph after the first call.
+
+    The forward issues some 60 small operations per layer; replaying them
+    as one graph removes the per-launch host cost.  Inputs are copied into
+    the static buffers before each replay; the KV cache, page tables and
+    context lengths are read from device memory by the kernels, so one
+    capture serves every step with the same (B, Q, table width).  Outputs
+    live in the graph's memory pool and are overwritten by the next replay.
+    """
+
+    def __init__(self, model: "Qwen3PagedModel", kv: PagedKV, B: int, Q: int, width: int, causal: bool,
+                 post=None, use_graph: bool = True):
+        dev = model.device
+        self.model, self.kv, self.causal, self.post, self.use_graph = model, kv, causal, post, use_graph
+        self.ids = torch.zeros(B, Q, dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(B, Q, dtype=torch.int64, device=dev)
+        self.tables = torch.zeros(B, width, dtype=torch.int32, device=dev)
+        self.slots = torch.zeros(B * Q, dtype=torch.int64, device=dev)
+        self.lens = torch.ones(B, dtype=torch.int32, device=dev)
+        self.max_ctx = width * kv.page_size
+        self.graph = None
+        self.out = None
+        self.workspaces: list = []
+
+    def _body(self):
+        hidden = self.model(self.ids, self.pos, self.kv, self.tables, self.lens, self.slots, causal=self.causal,
+                            max_context=self.max_ctx)
+        return self.post(hidden, self.ids) if self.post is not None else None
+
+    def _load(self, ids, pos, tables, slots, lens):
+        self.ids.copy_(ids, non_blocking=True)
+        self.pos.copy_(pos, non_blocking=True)
+        self.tables.copy_(tables, non_blocking=True)
+        self.slots.copy_(slots, non_blocking=True)
+        self.lens.copy_(lens, non_blocking=True)
+
+    def __call__(self, ids, pos, tables, slots, lens):
+        self._load(ids, pos, tables, slots, lens)
+        if not self.use_graph:
+            return self._body()
+        if self.graph is None:
+            cur = torch.cuda.current_stream(self.model.device)
+            side = _warmup_stream(self.model.device)
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):  # warm-up outside the capture
+                self._body()
+            cur.wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            # Workspaces used by the captured kernels belong to this step.
+            with _lib.capture_workspaces(self.workspaces), torch.cuda.graph(g):
+                self.out = self._body()
+            self.graph = g
+            # The warm-up may have updated the static inputs in place.
+            self._load(ids, pos, tables, slots, lens)
+        self.graph.replay()
+        return self.out
 
 
 def prefill(model: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], name: str, block: int = 16) -> torch.Tensor:

@@ -50,3 +50,20 @@ def test_engine_output_is_target_greedy_decoding():
     # Engine._accepted keeps the reference's list semantics.
     assert Engine._accepted([[5, 1, 2, 9]], [[1, 2, 7, 8]]) == [(3, 7)]
     assert Engine._accepted([[5, 1, 2]], [[1, 2, 4]]) == [(3, 4)]
+
+
+def test_graph_replay_matches_eager_engine():
+    """Every step replayed from HIP graphs gives the eager run's tokens."""
+    outs = []
+    for graphs in (False, True):
+        eng = Engine(TARGET, DRAFT, pages=256, seed=11, mask_id=999, use_graphs=graphs)
+        for m in (eng.target, eng.draft):
+            m.lm_head.mul_(20.0)
+        g = torch.Generator().manual_seed(4)
+        prompts = torch.randint(0, 999, (3, 48), generator=g).tolist()
+        res = eng.generate(prompts, max_new_tokens=30, ignore_eos=True)
+        outs.append([o["tokens"] for o in res["outputs"]])
+        # a second run on the same engine replays the cached graphs again
+        res2 = eng.generate(prompts, max_new_tokens=30, ignore_eos=True)
+        assert [o["tokens"] for o in res2["outputs"]] == outs[-1]
+    assert outs[0] == outs[1]

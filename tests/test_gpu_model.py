@@ -113,3 +113,22 @@ def test_denoise_loop_matches_restatement():
     again = dr.d3d_draft_block(model, kv, seqs, torch.full((2, 16), mask_id, dtype=torch.int64, device=dev), 4,
                                mask_id=mask_id)
     assert torch.equal(again, cur)
+
+
+def test_denoise_graph_replay_matches_eager():
+    dev = torch.device("cuda:0")
+    model = Qwen3PagedModel(TINY, dev, draft=True, seed=9, init_std=0.05)
+    model.lm_head.mul_(20.0)
+    kv = PagedKV(TINY, 64, 16, dev)
+    g = torch.Generator().manual_seed(2)
+    seqs = [Sequence(i, torch.randint(0, TINY.vocab - 1, (32,), generator=g).tolist()) for i in range(2)]
+    prefill(model, kv, seqs, "draft")
+    mask_id = TINY.vocab - 1
+    block = torch.full((2, 16), mask_id, dtype=torch.int64, device=dev)
+    eager = dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id)
+    graphs = {}
+    for _ in range(3):  # capture, then replays with eager work in between
+        got = dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id, graphs=graphs)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager)
+        assert torch.equal(dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id), eager)
