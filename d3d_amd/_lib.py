@@ -51,6 +51,12 @@ SIGNATURES = {
         _I,
         [_P, _I, _P, _I64, _I, _F, _I, _I, _I64, _P, _P, _P, _SZ, _P],
     ),
+    "d3d_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "d3d_qk_rope_append": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I64, _P],
+    ),
+    "d3d_silu_mul": (_I, [_P, _P, _I, _I, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -1,0 +1,228 @@
+// Fused per-layer glue of the Qwen3-shaped target and draft forwards.
+//
+// Each kernel replaces a chain of small tensor operations with one pass:
+//
+//   add_rmsnorm      residual += x (rounded to bf16), out = RMSNorm(sum) * w
+//                    serving/vendor/ssd/layers/layernorm.py:53-98 (RMSDNorm:
+//                    fp32 sum and statistics, bf16 normalised value times a
+//                    bf16 weight)
+//   qk_rope_append   per token: q/k head RMSNorm (RMSHeadNorm,
+//                    layernorm.py:1-52), rotary embedding, q written out, k and
+//                    v appended to the paged cache at the token's slot
+//                    (serving/vendor/ssd/layers/attention.py:21-22).  Target
+//                    RoPE rotates in fp32 (rotary_embedding.py:6-16); draft
+//                    RoPE follows models/d3d/modeling_d3d.py:164-187 with cos
+//                    and sin rounded to bf16 and each product rounded to bf16.
+//   silu_mul         out = silu(gate) * up computed in fp32 and rounded once
+//                    to bf16, as the compiled SiluAndMul of
+//                    serving/vendor/ssd/layers/activation.py:6-14 evaluates it
+//
+// Rows are bf16; the head dim is 128, split between lane l (entry l) and
+// lane l + 64 of a wave (entry l + 64), which are exactly the pairs the
+// rotate-half RoPE mixes.
+#include "d3d_common.hpp"
+#include "../../include/d3d_hip.h"
+
+namespace d3d {
+namespace layers {
+
+constexpr int NT = 256;
+constexpr int HD = 128;  // head dim
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
+__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// One workgroup per row of H entries (H a multiple of 8).
+__global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, uint16_t* residual,
+                                                         const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                         int H, float eps) {
+    const size_t row = blockIdx.x;
+    __shared__ float red[NT / kWave];
+    constexpr int kMaxVec = 4;  // up to 4 vectors of 8 per thread: H <= 8192
+    float v[kMaxVec][8];
+    const int nvec = H / 8;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxVec; ++j) {
+        const int vi = threadIdx.x + j * NT;
+        if (vi >= nvec) break;
+        const size_t off = row * H + vi * 8;
+        const u32x4 r = *reinterpret_cast<const u32x4*>(residual + off);
+        u32x4 a = {0u, 0u, 0u, 0u};
+        if (x) a = *reinterpret_cast<const u32x4*>(x + off);
+        u32x4 rs;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            float lo = bf16_bits_to_f32(r[h] & 0xffffu), hi = bf16_bits_to_f32(r[h] >> 16);
+            if (x) {
+                lo += bf16_bits_to_f32(a[h] & 0xffffu);
+                hi += bf16_bits_to_f32(a[h] >> 16);
+            }
+            v[j][2 * h] = lo;
+            v[j][2 * h + 1] = hi;
+            ss += lo * lo + hi * hi;
+            rs[h] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+        }
+        if (x) *reinterpret_cast<u32x4*>(residual + off) = rs;
+    }
+    const float tot = block_sum<NT>(ss, red);
+    const float rstd = rsqrtf(tot / (float)H + eps);
+#pragma unroll
+    for (int j = 0; j < kMaxVec; ++j) {
+        const int vi = threadIdx.x + j * NT;
+        if (vi >= nvec) break;
+        const size_t off = row * H + vi * 8;
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(w + vi * 8);
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float lo = rbf(v[j][2 * h] * rstd) * bf16_bits_to_f32(wv[h] & 0xffffu);
+            const float hi = rbf(v[j][2 * h + 1] * rstd) * bf16_bits_to_f32(wv[h] >> 16);
+            o[h] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+        }
+        *reinterpret_cast<u32x4*>(out + off) = o;
+    }
+}
+
+// One workgroup per token; wave w handles heads w, w + 4, ...: query heads
+// (norm + rope -> q_out), key heads (norm + rope -> k_cache) and value heads
+// (copy -> v_cache).
+template <bool DRAFT_ROPE>
+__global__ __launch_bounds__(NT) void qk_rope_append_kernel(
+    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ positions, const uint16_t* __restrict__ qn,
+    const uint16_t* __restrict__ kn, const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out,
+    uint16_t* k_cache, uint16_t* v_cache, const int64_t* __restrict__ slots, int Hq, int Hkv, float eps,
+    int64_t num_slots) {
+    const size_t t = blockIdx.x;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __shared__ float cs[HD / 2], sn[HD / 2];
+    const int64_t pos = positions[t];
+    if (threadIdx.x < HD / 2) {
+        const float f = (float)pos * inv_freq[threadIdx.x];
+        cs[threadIdx.x] = cosf(f);
+        sn[threadIdx.x] = sinf(f);
+    }
+    __syncthreads();
+    const int64_t slot = slots[t];
+    const bool store = slot >= 0 && slot < num_slots;
+    const uint16_t* row = qkv + t * (size_t)(Hq + 2 * Hkv) * HD;
+    const int heads = Hq + 2 * Hkv;
+    for (int h = wv; h < heads; h += NT / kWave) {
+        const uint16_t* src = row + (size_t)h * HD;
+        const uint16_t a = src[lane], b = src[lane + 64];
+        if (h >= Hq + Hkv) {  // value head: copy into the cache
+            if (store) {
+                uint16_t* dst = v_cache + ((size_t)slot * Hkv + (h - Hq - Hkv)) * HD;
+                dst[lane] = a;
+                dst[lane + 64] = b;
+            }
+            continue;
+        }
+        const bool is_q = h < Hq;
+        const float x0 = bf(a), x1 = bf(b);
+        const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
+        const uint16_t* nw = is_q ? qn : kn;
+        const float y0 = rbf(rbf(x0 * rstd) * bf(nw[lane]));
+        const float y1 = rbf(rbf(x1 * rstd) * bf(nw[lane + 64]));
+        float o0, o1;
+        if constexpr (DRAFT_ROPE) {
+            const float c = rbf(cs[lane]), s = rbf(sn[lane]);
+            o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
+            o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
+        } else {
+            const float c = cs[lane], s = sn[lane];
+            o0 = y0 * c - y1 * s;
+            o1 = y1 * c + y0 * s;
+        }
+        uint16_t* dst;
+        if (is_q) {
+            dst = q_out + (t * Hq + h) * HD;
+        } else {
+            if (!store) continue;
+            dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
+        }
+        dst[lane] = f32_to_bf16_bits(o0);
+        dst[lane + 64] = f32_to_bf16_bits(o1);
+    }
+}
+
+// out[t, i] = silu(gate[t, i]) * up[t, i] with gate_up = [gate | up] per row.
+__global__ __launch_bounds__(NT) void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                      int M, size_t total_vec) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= total_vec) return;
+    const int mv = M / 8;
+    const size_t t = i / mv, c = i % mv;
+    const u32x4 g = *reinterpret_cast<const u32x4*>(gu + t * 2 * M + c * 8);
+    const u32x4 u = *reinterpret_cast<const u32x4*>(gu + t * 2 * M + M + c * 8);
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        float r[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float gv = bf16_bits_to_f32(k ? (g[h] >> 16) : (g[h] & 0xffffu));
+            const float uv = bf16_bits_to_f32(k ? (u[h] >> 16) : (u[h] & 0xffffu));
+            r[k] = gv / (1.0f + expf(-gv)) * uv;
+        }
+        o[h] = (uint32_t)f32_to_bf16_bits(r[0]) | ((uint32_t)f32_to_bf16_bits(r[1]) << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + t * M + c * 8) = o;
+}
+
+}  // namespace layers
+}  // namespace d3d
+
+using namespace d3d;
+
+extern "C" int d3d_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int T, int H,
+                               float eps, void* stream) {
+    if (T < 0 || H < 8 || H % 8 || H > 8 * 4 * layers::NT) return D3D_E_SHAPE;
+    if (T == 0) return D3D_OK;
+    if (!residual || !weight || !out) return D3D_E_NULL;
+    hipLaunchKernelGGL(layers::add_rmsnorm_kernel, dim3(T), dim3(layers::NT), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
+                       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), H, eps);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}
+
+extern "C" int d3d_qk_rope_append(const void* qkv, const int64_t* positions, const void* q_norm_w,
+                                  const void* k_norm_w, const float* inv_freq, void* q_out, void* k_cache,
+                                  void* v_cache, const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
+                                  float eps, int draft_rope, int64_t num_slots, void* stream) {
+    if (T < 0 || Hq < 1 || Hkv < 1 || num_slots < 1) return D3D_E_SHAPE;
+    if (D != layers::HD) return D3D_E_UNSUPPORTED;
+    if (T == 0) return D3D_OK;
+    if (!qkv || !positions || !q_norm_w || !k_norm_w || !inv_freq || !q_out || !k_cache || !v_cache ||
+        !slot_mapping)
+        return D3D_E_NULL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* a = static_cast<const uint16_t*>(qkv);
+    if (draft_rope)
+        hipLaunchKernelGGL(layers::qk_rope_append_kernel<true>, dim3(T), dim3(layers::NT), 0, s, a, positions,
+                           static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
+                           inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
+                           static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
+    else
+        hipLaunchKernelGGL(layers::qk_rope_append_kernel<false>, dim3(T), dim3(layers::NT), 0, s, a, positions,
+                           static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
+                           inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
+                           static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}
+
+extern "C" int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream) {
+    if (T < 0 || M < 8 || M % 8) return D3D_E_SHAPE;
+    if (T == 0) return D3D_OK;
+    if (!gate_up || !out) return D3D_E_NULL;
+    const size_t total = (size_t)T * (M / 8);
+    const unsigned grid = (unsigned)((total + layers::NT - 1) / layers::NT);
+    hipLaunchKernelGGL(layers::silu_mul_kernel, dim3(grid), dim3(layers::NT), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), M, total);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}

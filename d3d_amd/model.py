@@ -1,7 +1,8 @@
 """Qwen3-shaped paged models for the verify (target) and draft forwards.
 
-Host code in PyTorch-ROCm (GEMMs on hipBLASLt); attention, KV append and
-the speculative reductions run on the gfx950 kernels.  Weights are
+Host code in PyTorch-ROCm (GEMMs on hipBLASLt); attention, the norms,
+RoPE with the KV append, SiLU-mul and the speculative reductions run on the
+gfx950 kernels.  Weights are
 random-initialised bf16 (there are no checkpoints on this path's benchmarks).
 
 Reference structure followed:
@@ -26,7 +27,6 @@ exactly causal attention over the prompt.
 """
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -35,6 +35,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import attention as att
+from . import layers as ly
 
 
 @dataclass(frozen=True)
@@ -119,59 +120,35 @@ class Qwen3PagedModel(torch.nn.Module):
         self.inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, half, device=self.device,
                                                                    dtype=torch.float32) * 2 / d))
 
-    # -- layers ---------------------------------------------------------------
-    def _rms(self, x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.shape.eps)
-        return xf.to(x.dtype) * weight
-
-    def _rope(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """x [T, H, D]; positions [T]."""
-        freqs = positions.float()[:, None] * self.inv_freq[None, :]
-        cos, sin = freqs.cos()[:, None, :], freqs.sin()[:, None, :]
-        if self.draft:
-            # HF apply_rotary_pos_emb with cos/sin cast to the activation dtype.
-            cos2 = torch.cat([cos, cos], -1).to(x.dtype)
-            sin2 = torch.cat([sin, sin], -1).to(x.dtype)
-            x1, x2 = x.chunk(2, dim=-1)
-            return x * cos2 + torch.cat([-x2, x1], -1) * sin2
-        x1, x2 = x.float().chunk(2, dim=-1)
-        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1).to(x.dtype)
-
     def forward(self, ids: torch.Tensor, positions: torch.Tensor, kv: PagedKV, block_tables: torch.Tensor,
                 context_lens: torch.Tensor, slot_mapping: torch.Tensor, *, causal: bool,
                 max_context: int) -> torch.Tensor:
         """Hidden states [B, Q, hidden] of a block of Q tokens per request.
 
         The block's K/V are appended at ``slot_mapping`` before attention;
-        ``context_lens`` counts the prefix plus the block.
+        ``context_lens`` counts the prefix plus the block.  Per layer: fused
+        add + RMSNorm, QKV GEMM, fused q/k norm + RoPE + KV append, paged
+        attention, O GEMM, fused add + RMSNorm, gate-up GEMM, fused SiLU-mul,
+        down GEMM (the decoder layer of serving/vendor/ssd/models/qwen3.py).
         """
         B, Q = ids.shape
         s = self.shape
         Hq, Hkv, d = s.heads, s.kv_heads, s.head_dim
         pos = positions.reshape(-1)
-        x = F.embedding(ids.reshape(-1), self.embed)
-        residual = None
+        residual = F.embedding(ids.reshape(-1), self.embed)  # updated in place below
+        hs = torch.empty_like(residual)
+        x = None
         for li, L in enumerate(self.layers):
-            if residual is None:
-                residual = x
-            else:
-                residual = residual + x
-            hs = self._rms(residual, L["ln1"])
+            ly.add_rmsnorm(x, residual, L["ln1"], s.eps, out=hs)
             qkv = F.linear(hs, L["qkv"])
-            q, k, v = qkv.split([Hq * d, Hkv * d, Hkv * d], dim=-1)
-            q = self._rope(self._rms(q.reshape(-1, Hq, d), L["qn"]), pos)
-            k = self._rope(self._rms(k.reshape(-1, Hkv, d), L["kn"]), pos)
-            att.kv_append(k, v.reshape(-1, Hkv, d), kv.k[li], kv.v[li], slot_mapping)
-            o = att.flash_attn_with_kvcache(q.reshape(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens,
+            q = ly.qk_rope_append(qkv, pos, L["qn"], L["kn"], self.inv_freq, kv.k[li], kv.v[li], slot_mapping,
+                                  Hq, Hkv, s.eps, draft_rope=self.draft)
+            o = att.flash_attn_with_kvcache(q.view(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens,
                                             block_tables, causal=causal, max_seqlen_k=max_context)
             x = F.linear(o.reshape(B * Q, Hq * d), L["o"])
-            residual = residual + x
-            hs = self._rms(residual, L["ln2"])
-            gu = F.linear(hs, L["gate_up"])
-            gate, up = gu.chunk(2, dim=-1)
-            x = F.linear(F.silu(gate) * up, L["down"])
-        out = self._rms(residual + x, self.norm)
+            ly.add_rmsnorm(x, residual, L["ln2"], s.eps, out=hs)
+            x = F.linear(ly.silu_mul(F.linear(hs, L["gate_up"])), L["down"])
+        out = ly.add_rmsnorm(x, residual, self.norm, s.eps)
         return out.reshape(B, Q, s.hidden)
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:

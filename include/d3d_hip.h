@@ -173,6 +173,44 @@ int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids
                                float* conf_out, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/*
+ * Residual add + RMSNorm over rows of H bf16 entries (H a multiple of 8,
+ * H <= 8192): s = x + residual in fp32, residual = bf16(s) (in place),
+ * out = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight).  With x == NULL the
+ * residual is only normalised (the first layer's input norm) and left as is.
+ *
+ * Replaces RMSDNorm.add_norm_forward / norm_forward,
+ * serving/vendor/ssd/layers/layernorm.py:53-98, as called by the decoder
+ * layers of serving/vendor/ssd/models/qwen3.py and the draft's
+ * models/d3d/modeling_d3d.py.
+ */
+int d3d_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int T, int H,
+                    float eps, void* stream);
+
+/*
+ * Per-token attention input: for each of T tokens, qkv [T, (Hq + 2 Hkv) * D]
+ * bf16 holds q, k and v heads.  q and k heads get RMSNorm over D with
+ * q_norm_w / k_norm_w (RMSHeadNorm, serving/vendor/ssd/layers/layernorm.py:1-52)
+ * and rotate-half RoPE at positions[t] with angle positions[t] * inv_freq[i]
+ * (inv_freq [D/2] fp32).  draft_rope == 0 rotates in fp32 and rounds once
+ * (serving/vendor/ssd/layers/rotary_embedding.py:6-16); draft_rope != 0
+ * rounds cos, sin and every product and sum to bf16
+ * (models/d3d/modeling_d3d.py:164-187).  q goes to q_out [T, Hq, D]; k and
+ * v go to the paged caches at slot_mapping[t] as d3d_kv_append stores them
+ * (serving/vendor/ssd/layers/attention.py:21-22).  D must be 128.
+ */
+int d3d_qk_rope_append(const void* qkv, const int64_t* positions, const void* q_norm_w,
+                       const void* k_norm_w, const float* inv_freq, void* q_out, void* k_cache,
+                       void* v_cache, const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
+                       float eps, int draft_rope, int64_t num_slots, void* stream);
+
+/*
+ * out [T, M] = silu(gate) * up for gate_up [T, 2M] = [gate | up] bf16,
+ * evaluated in fp32 and rounded once (SiluAndMul,
+ * serving/vendor/ssd/layers/activation.py:6-14).  M a multiple of 8.
+ */
+int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
