@@ -36,6 +36,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _I, _I, _P, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
+    "d3d_accept_fused_sparse": (
+        _I,
+        [_P, _I, _I, _P, _P, _P, _I, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
     "d3d_attn_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
     "d3d_verify_attn_paged": (
         _I,

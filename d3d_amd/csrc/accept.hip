@@ -28,6 +28,14 @@
 //                                         mass <= 1e-12 fallback, resample
 //   single/eval_sync.py:1223-1234         greedy leading-match acceptance
 //
+// Sparse proposals (single/speculative_sampling.py:79-143): the draft side is
+// a support of S (id, probability) pairs per position instead of a dense row.
+// Phase 1 then reads target rows only; phase 2 computes q at the draft token
+// as the normalised support mass on that id, and the residual of the reject
+// row subtracts the normalised support from p entry by entry, in support
+// order (scatter_add), before the clamp at zero.  Ids outside [0, V) carry
+// no mass.
+//
 // Every reduction runs in one fixed order for a given (V, dtype), so outputs
 // are deterministic.  The stochastic draw replaces torch.multinomial with an
 // inverse CDF over the unnormalised weights driven by resample_u:
@@ -49,11 +57,13 @@ constexpr int kMaxK = 127;       // K+1 target rows + K draft rows <= 255
 // chunks (more workgroups, shorter per-thread chains), many requests get
 // coarse ones (fewer redundant row merges).
 constexpr int kMaxNv2 = 4;
+constexpr int kMaxS = 1024;  // sparse support entries per position
 
 struct Decision {
     int n;  // first rejected position (K when all accepted)
     int flags;
     float Mt, St, Mq, Sq;  // row statistics of the selected target/draft rows
+                           // (sparse proposals: Sq = support mass of the reject row)
     int pad0, pad1;
 };
 
@@ -82,6 +92,9 @@ struct Params {
     Decision* dec;   // [B]
     ResStat* rstats; // [B][C]
     float* xtok;     // [B][R]: value of row r at its draft token (rows != K)
+    const int64_t* q_ids;  // sparse proposals [B][K][S], else null
+    const float* q_probs;  // [B][K][S]
+    int S;
     int32_t* accepted;
     uint8_t* mask;
     int64_t* out_token;
@@ -118,20 +131,64 @@ __global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
     }
 }
 
+// ---------------------------------------------------------------- sparse
+// Support mass Z = max(sum_s q_s, 1e-12) of position i and the normalised
+// mass on token tok (sum over matching ids of q_s / Z), one wave per call.
+__device__ __forceinline__ void sparse_q_at(const Params& P, int b, int i, int64_t tok, float& Z, float& qt) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t row = ((size_t)b * P.K + i) * P.S;
+    float z = 0.f;
+    for (int s = lane; s < P.S; s += kWave) z += P.q_probs[row + s];
+    Z = fmaxf(wave_sum(z), 1e-12f);
+    float m = 0.f;
+    for (int s = lane; s < P.S; s += kWave)
+        if (P.q_ids[row + s] == tok) m += P.q_probs[row + s] / Z;
+    qt = wave_sum(m);
+}
+
+// Residual weights of a sparse proposal over entries [lo, lo + span): buf
+// holds p at local index e - lo on entry and p - sum(q_s / Z) (support
+// order, unclamped) at every support id on exit.  Block-wide; every thread
+// must call it.
+__device__ __forceinline__ void sparse_subtract(const Params& P, int b, int n, float Z, int lo, int span,
+                                                float* buf, int* s_id, float* s_q) {
+    const size_t row = ((size_t)b * P.K + n) * P.S;
+    for (int s = threadIdx.x; s < P.S; s += NT) {
+        const int64_t id = P.q_ids[row + s];
+        s_id[s] = (id >= lo && id < (int64_t)lo + span && id < P.V) ? (int)(id - lo) : -1;
+        s_q[s] = P.q_probs[row + s] / Z;
+    }
+    __syncthreads();
+    for (int s = threadIdx.x; s < P.S; s += NT) {
+        const int li = s_id[s];
+        if (li < 0) continue;
+        bool first = true;
+        for (int t = 0; t < s && first; ++t) first = s_id[t] != li;
+        if (!first) continue;  // the first occurrence applies every duplicate, in order
+        float v = buf[li];
+        for (int t = s; t < P.S; ++t)
+            if (s_id[t] == li) v -= s_q[t];
+        buf[li] = v;
+    }
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------- phase 2
 // Row statistics of request b: sM/sS per row (target rows 0..K, draft rows
 // K+1..2K) and sArg for target rows.
-template <Mode M>
+template <Mode M, bool SP>
 __device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, float* sS, int* sArg,
                                            RowStat* lds) {
     const int K = P.K, C = P.C, R = 2 * K + 1;
-    merge_row_stats<M>(P.stats + (size_t)b * R * C, M == kGreedy ? K + 1 : R, C, K + 1, sM, sS, sArg, lds);
+    merge_row_stats<M>(P.stats + (size_t)b * R * C, (M == kGreedy || SP) ? K + 1 : R, C, K + 1, sM, sS, sArg,
+                       lds);
 }
 
-template <int DT, bool VEC, Mode M, bool UNIT_T>
+template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
 __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowStat* lds, float* sM, float* sS,
                                             int* sArg, uint8_t* sAcc, uint8_t* sBad, int* s_flags, float* rf,
                                             int* ri) {
+    __shared__ float sQt[SP ? kMaxK : 1], sZ[SP ? kMaxK : 1];
     constexpr int E = Vec<DT>::E;
     const int K = P.K, V = P.V, C = P.C;
     const int tid = threadIdx.x;
@@ -144,10 +201,22 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         if (M != kGreedy) {
             u = P.uniforms[(size_t)b * K + tid];
             xt = P.xtok[(size_t)b * (2 * K + 1) + tid];
-            xq = P.xtok[(size_t)b * (2 * K + 1) + K + 1 + tid];
+            if (!SP) xq = P.xtok[(size_t)b * (2 * K + 1) + K + 1 + tid];
         }
     }
-    merge_rows<M>(P, b, sM, sS, sArg, lds);
+    if constexpr (SP) {
+        // q at the draft token of every position, one wave per position.
+        for (int i = tid / kWave; i < K; i += NT / kWave) {
+            float Z, qt;
+            sparse_q_at(P, b, i, P.tokens[(size_t)b * K + i], Z, qt);
+            if ((tid & (kWave - 1)) == 0) {
+                sZ[i] = Z;
+                sQt[i] = qt;
+            }
+        }
+    }
+    merge_rows<M, SP>(P, b, sM, sS, sArg, lds);
+    if constexpr (SP) __syncthreads();
 
     if (tid < K) {
         const bool bad = tok < 0 || tok >= V;
@@ -157,7 +226,8 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         } else {
             if (!bad) {
                 const float pt = prob_of<M, UNIT_T>(xt, sM[tid], inv_sum<M>(sS[tid]), P.T);
-                const float qt = prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
+                const float qt = SP ? sQt[tid]
+                                    : prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
                 const float a = fminf(1.0f, pt / fmaxf(qt, 1e-12f));
                 acc = u <= a;
             }
@@ -194,8 +264,8 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
                 d.flags = bad ? kFlagInvalid : 0;
                 d.Mt = sM[n];
                 d.St = sS[n];
-                d.Mq = n < K ? sM[K + 1 + n] : 0.f;
-                d.Sq = n < K ? sS[K + 1 + n] : 0.f;
+                d.Mq = (n < K && !SP) ? sM[K + 1 + n] : 0.f;
+                d.Sq = n < K ? (SP ? sZ[n] : sS[K + 1 + n]) : 0.f;
                 d.pad0 = d.pad1 = 0;
                 P.dec[b] = d;
             }
@@ -206,9 +276,10 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         // Chunk sums of the selected row pair (reject row, or bonus row).
         const bool res = n < K;
         const void* trow = row_ptr<DT>(P.target, (size_t)b * (K + 1) + n, V);
-        const void* drow = res ? row_ptr<DT>(P.draft, (size_t)b * K + n, V) : nullptr;
+        const bool dres = res && !SP;  // dense draft row to read
+        const void* drow = dres ? row_ptr<DT>(P.draft, (size_t)b * K + n, V) : nullptr;
         const float Mt = sM[n], It = inv_sum<M>(sS[n]);
-        const float Mq = res ? sM[K + 1 + n] : 0.f, Iq = res ? inv_sum<M>(sS[K + 1 + n]) : 0.f;
+        const float Mq = dres ? sM[K + 1 + n] : 0.f, Iq = dres ? inv_sum<M>(sS[K + 1 + n]) : 0.f;
         // Workgroup c covers sub-chunks c*nv2 .. c*nv2+nv2-1; sub-chunk j is
         // vector j of every thread (NT*E consecutive entries) and gets its own
         // record, so phase 3 always scans one vector per thread.
@@ -217,7 +288,25 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         const int first = c * (NT * E * nv2) + tid * E;
         float xt[LM], xq[LM];
         load_tile_n<DT, VEC, LM>(trow, V, first, NT * E, nv2, fill_value<M>(), xt);
-        if (res) load_tile_n<DT, VEC, LM>(drow, V, first, NT * E, nv2, fill_value<M>(), xq);
+        if (dres) load_tile_n<DT, VEC, LM>(drow, V, first, NT * E, nv2, fill_value<M>(), xq);
+        if constexpr (SP) {
+            // xq <- p - q (unclamped) through the workgroup's LDS copy of p.
+            __shared__ float buf[NT * kMaxNv2 * E];
+            __shared__ int s_id[kMaxS];
+            __shared__ float s_q[kMaxS];
+            const int lo = c * (NT * E * nv2);
+#pragma unroll
+            for (int j = 0; j < kMaxNv2; ++j)
+#pragma unroll
+                for (int k = 0; k < E; ++k)
+                    if (j < nv2) buf[j * NT * E + tid * E + k] = prob_of<M, UNIT_T>(xt[j * E + k], Mt, It, P.T);
+            if (res) sparse_subtract(P, b, n, sZ[n], lo, NT * E * nv2, buf, s_id, s_q);
+#pragma unroll
+            for (int j = 0; j < kMaxNv2; ++j)
+#pragma unroll
+                for (int k = 0; k < E; ++k)
+                    if (j < nv2) xq[j * E + k] = buf[j * NT * E + tid * E + k];
+        }
         float rs[kMaxNv2], ps[kMaxNv2];
         int lr[kMaxNv2], lp[kMaxNv2];
 #pragma unroll
@@ -233,7 +322,7 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
                 ps[j] += p;
                 if (p > 0.f) lp[j] = e;
                 if (res) {
-                    const float r = fmaxf(p - prob_of<M, UNIT_T>(xq[l], Mq, Iq, P.T), 0.f);
+                    const float r = SP ? fmaxf(xq[l], 0.f) : fmaxf(p - prob_of<M, UNIT_T>(xq[l], Mq, Iq, P.T), 0.f);
                     rs[j] += r;
                     if (r > 0.f) lr[j] = e;
                 }
@@ -270,7 +359,7 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
     }
 }
 
-template <int DT, bool VEC, Mode M>
+template <int DT, bool VEC, Mode M, bool SP>
 __global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
     __shared__ RowStat lds[kMaxStatLds];
     __shared__ float sM[2 * kMaxK + 2], sS[2 * kMaxK + 2];
@@ -280,13 +369,15 @@ __global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
     __shared__ float rf[NT / kWave];
     __shared__ int ri[NT / kWave];
     if (P.T == 1.0f)
-        decide_body<DT, VEC, M, true>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf, ri);
+        decide_body<DT, VEC, M, true, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf,
+                                          ri);
     else
-        decide_body<DT, VEC, M, false>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf, ri);
+        decide_body<DT, VEC, M, false, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf,
+                                           ri);
 }
 
 // ---------------------------------------------------------------- phase 3
-template <int DT, bool VEC, Mode M, bool UNIT_T>
+template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
 __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_wave, float* s_f, int* s_i,
                                               int* ri) {
     constexpr int E = Vec<DT>::E;
@@ -301,7 +392,7 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
     if (tid < C) mine0 = P.rstats[(size_t)b * C + tid];
     if (d.flags & kFlagInvalid) return;
     const bool res = d.n < K;
-    const float It = inv_sum<M>(d.St), Iq = res ? inv_sum<M>(d.Sq) : 0.f;
+    const float It = inv_sum<M>(d.St), Iq = (res && !SP) ? inv_sum<M>(d.Sq) : 0.f;
 
     // Chunk-level inverse CDF: inclusive scan of chunk sums in chunk order,
     // the crossing chunk is the first whose inclusive sum exceeds v * W.
@@ -369,15 +460,28 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
         float xt[E], xq[E];
         load_tile<DT, VEC, false, E>(row_ptr<DT>(P.target, (size_t)b * (K + 1) + d.n, V), V, first, E,
                                      fill_value<M>(), xt);
-        if (res)
+        if (res && !SP)
             load_tile<DT, VEC, false, E>(row_ptr<DT>(P.draft, (size_t)b * K + d.n, V), V, first, E,
                                          fill_value<M>(), xq);
         float w[E];
+        if constexpr (SP) {
+            __shared__ float buf[NT * E];
+            __shared__ int s_id[kMaxS];
+            __shared__ float s_q[kMaxS];
+#pragma unroll
+            for (int l = 0; l < E; ++l) buf[tid * E + l] = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
+            if (use_r) sparse_subtract(P, b, d.n, d.Sq, cs * (NT * E), NT * E, buf, s_id, s_q);
+            else __syncthreads();
+#pragma unroll
+            for (int l = 0; l < E; ++l) w[l] = use_r ? fmaxf(buf[tid * E + l], 0.f) : buf[tid * E + l];
+        }
         float tsum = 0.f;
 #pragma unroll
         for (int l = 0; l < E; ++l) {
-            const float p = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
-            w[l] = use_r ? fmaxf(p - prob_of<M, UNIT_T>(xq[l], d.Mq, Iq, P.T), 0.f) : p;
+            if constexpr (!SP) {
+                const float p = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
+                w[l] = use_r ? fmaxf(p - prob_of<M, UNIT_T>(xq[l], d.Mq, Iq, P.T), 0.f) : p;
+            }
             tsum += w[l];
         }
         const float incl = block_incl_scan(tsum, s_wave);
@@ -398,16 +502,16 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
     if (tid == 0) P.out_token[b] = token;
 }
 
-template <int DT, bool VEC, Mode M>
+template <int DT, bool VEC, Mode M, bool SP>
 __global__ __launch_bounds__(NT) void accept_resample_kernel(Params P) {
     __shared__ float s_wave[NT / kWave];
     __shared__ float s_f[4];
     __shared__ int s_i[2];
     __shared__ int ri[NT / kWave];
     if (P.T == 1.0f)
-        resample_body<DT, VEC, M, true>(P, blockIdx.x, s_wave, s_f, s_i, ri);
+        resample_body<DT, VEC, M, true, SP>(P, blockIdx.x, s_wave, s_f, s_i, ri);
     else
-        resample_body<DT, VEC, M, false>(P, blockIdx.x, s_wave, s_f, s_i, ri);
+        resample_body<DT, VEC, M, false, SP>(P, blockIdx.x, s_wave, s_f, s_i, ri);
 }
 
 struct Layout {
@@ -437,29 +541,95 @@ static Layout layout(int B, int K, int64_t V) {
     return l;
 }
 
-template <int DT, bool VEC>
+template <int DT, bool VEC, bool SP>
 static hipError_t launch(const Params& P, Mode mode, int B, hipStream_t stream) {
     const dim3 block(NT);
     const dim3 grid_dec(mode == kGreedy ? 1 : (P.C2 + P.nv2 - 1) / P.nv2, B);
+    // Target rows 0..K, then (dense proposals) draft rows.
+    const dim3 grid_stats(P.C, (mode == kGreedy || SP) ? P.K + 1 : 2 * P.K + 1, B);
     switch (mode) {
         case kGreedy:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kGreedy>), dim3(P.C, P.K + 1, B), block, 0,
-                               stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kGreedy>), grid_dec, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kGreedy>), grid_stats, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kGreedy, false>), grid_dec, block, 0, stream, P);
             return hipGetLastError();
         case kLogits:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kLogits>), dim3(P.C, 2 * P.K + 1, B), block, 0,
-                               stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kLogits>), grid_dec, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kLogits>), dim3(B), block, 0, stream, P);
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kLogits>), grid_stats, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kLogits, SP>), grid_dec, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kLogits, SP>), dim3(B), block, 0, stream, P);
             return hipGetLastError();
         default:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kProbs>), dim3(P.C, 2 * P.K + 1, B), block, 0,
-                               stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kProbs>), grid_dec, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kProbs>), dim3(B), block, 0, stream, P);
+            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kProbs>), grid_stats, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kProbs, SP>), grid_dec, block, 0, stream, P);
+            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kProbs, SP>), dim3(B), block, 0, stream, P);
             return hipGetLastError();
     }
+}
+
+// Shared by the dense and sparse entry points: validation, workspace carving
+// and dispatch.
+static int run(const void* target, const void* draft, const int64_t* q_ids, const float* q_probs, int S,
+               int dtype, int input_kind, const int64_t* draft_tokens, const float* uniforms,
+               const float* resample_u, float temperature, int B, int K, int64_t V, int32_t* accepted,
+               uint8_t* accept_mask, int64_t* out_token, uint8_t* all_accepted, int64_t* posterior,
+               void* workspace, size_t workspace_bytes, void* stream) {
+    const bool sparse = q_ids != nullptr || q_probs != nullptr || S != 0;
+    if (B < 1 || B > 65535 || K < 1 || K > kMaxK || V < 1 || V > (int64_t)kMaxStatLds * kChunk)
+        return D3D_E_SHAPE;
+    if (sparse && (S < 1 || S > kMaxS)) return D3D_E_SHAPE;
+    if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
+    if (input_kind != D3D_INPUT_LOGITS && input_kind != D3D_INPUT_PROBS) return D3D_E_UNSUPPORTED;
+    const bool greedy = input_kind == D3D_INPUT_LOGITS && !(temperature > 1e-5f);
+    if (!target || !draft_tokens || !accepted || !accept_mask || !out_token || !all_accepted || !workspace)
+        return D3D_E_NULL;
+    if (!greedy && (!uniforms || !resample_u)) return D3D_E_NULL;
+    if (!greedy && (sparse ? (!q_ids || !q_probs) : !draft)) return D3D_E_NULL;
+    const Layout lay = layout(B, K, V);
+    if (workspace_bytes < lay.total) return D3D_E_WORKSPACE;
+
+    char* ws = static_cast<char*>(workspace);
+    Params P;
+    P.target = target;
+    P.draft = (greedy || sparse) ? nullptr : draft;
+    P.tokens = draft_tokens;
+    P.uniforms = uniforms;
+    P.resample_u = resample_u;
+    P.T = input_kind == D3D_INPUT_LOGITS ? temperature : 1.0f;
+    P.K = K;
+    P.V = (int)V;
+    P.C = num_chunks(V);
+    P.nv2 = pick_nv2(B);
+    P.C2 = num_subchunks(V, dtype);
+    P.stats = reinterpret_cast<RowStat*>(ws + lay.stats);
+    P.dec = reinterpret_cast<Decision*>(ws + lay.dec);
+    P.rstats = reinterpret_cast<ResStat*>(ws + lay.rstats);
+    P.xtok = reinterpret_cast<float*>(ws + lay.xtok);
+    P.q_ids = sparse ? q_ids : nullptr;
+    P.q_probs = sparse ? q_probs : nullptr;
+    P.S = sparse ? S : 0;
+    P.accepted = accepted;
+    P.mask = accept_mask;
+    P.out_token = out_token;
+    P.all_accepted = all_accepted;
+    P.posterior = posterior;
+
+    const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;
+    const bool vec = ((uintptr_t)target % 16 == 0) && (greedy || sparse || (uintptr_t)draft % 16 == 0) &&
+                     ((size_t)V * esize) % 16 == 0;
+    const Mode mode = greedy ? kGreedy : (input_kind == D3D_INPUT_PROBS ? kProbs : kLogits);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (dtype == D3D_DTYPE_F32) {
+        if (sparse)
+            err = vec ? launch<kF32, true, true>(P, mode, B, s) : launch<kF32, false, true>(P, mode, B, s);
+        else
+            err = vec ? launch<kF32, true, false>(P, mode, B, s) : launch<kF32, false, false>(P, mode, B, s);
+    } else {
+        if (sparse)
+            err = vec ? launch<kBF16, true, true>(P, mode, B, s) : launch<kBF16, false, true>(P, mode, B, s);
+        else
+            err = vec ? launch<kBF16, true, false>(P, mode, B, s) : launch<kBF16, false, false>(P, mode, B, s);
+    }
+    return err == hipSuccess ? D3D_OK : (int)err;
 }
 
 }  // namespace accept
@@ -478,50 +648,19 @@ extern "C" int d3d_accept_fused(const void* target, const void* draft, int dtype
                                 int32_t* accepted, uint8_t* accept_mask, int64_t* out_token,
                                 uint8_t* all_accepted, int64_t* posterior, void* workspace,
                                 size_t workspace_bytes, void* stream) {
-    using namespace accept;
-    if (B < 1 || B > 65535 || K < 1 || K > kMaxK || V < 1 || V > (int64_t)kMaxStatLds * kChunk)
-        return D3D_E_SHAPE;
-    if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
-    if (input_kind != D3D_INPUT_LOGITS && input_kind != D3D_INPUT_PROBS) return D3D_E_UNSUPPORTED;
-    const bool greedy = input_kind == D3D_INPUT_LOGITS && !(temperature > 1e-5f);
-    if (!target || !draft_tokens || !accepted || !accept_mask || !out_token || !all_accepted || !workspace)
-        return D3D_E_NULL;
-    if (!greedy && (!draft || !uniforms || !resample_u)) return D3D_E_NULL;
-    const Layout lay = layout(B, K, V);
-    if (workspace_bytes < lay.total) return D3D_E_WORKSPACE;
+    return accept::run(target, draft, nullptr, nullptr, 0, dtype, input_kind, draft_tokens, uniforms, resample_u,
+                       temperature, B, K, V, accepted, accept_mask, out_token, all_accepted, posterior, workspace,
+                       workspace_bytes, stream);
+}
 
-    char* ws = static_cast<char*>(workspace);
-    Params P;
-    P.target = target;
-    P.draft = greedy ? nullptr : draft;
-    P.tokens = draft_tokens;
-    P.uniforms = uniforms;
-    P.resample_u = resample_u;
-    P.T = input_kind == D3D_INPUT_LOGITS ? temperature : 1.0f;
-    P.K = K;
-    P.V = (int)V;
-    P.C = num_chunks(V);
-    P.nv2 = pick_nv2(B);
-    P.C2 = num_subchunks(V, dtype);
-    P.stats = reinterpret_cast<RowStat*>(ws + lay.stats);
-    P.dec = reinterpret_cast<Decision*>(ws + lay.dec);
-    P.rstats = reinterpret_cast<ResStat*>(ws + lay.rstats);
-    P.xtok = reinterpret_cast<float*>(ws + lay.xtok);
-    P.accepted = accepted;
-    P.mask = accept_mask;
-    P.out_token = out_token;
-    P.all_accepted = all_accepted;
-    P.posterior = posterior;
-
-    const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;
-    const bool vec = ((uintptr_t)target % 16 == 0) && (greedy || (uintptr_t)draft % 16 == 0) &&
-                     ((size_t)V * esize) % 16 == 0;
-    const Mode mode = greedy ? kGreedy : (input_kind == D3D_INPUT_PROBS ? kProbs : kLogits);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t err;
-    if (dtype == D3D_DTYPE_F32)
-        err = vec ? launch<kF32, true>(P, mode, B, s) : launch<kF32, false>(P, mode, B, s);
-    else
-        err = vec ? launch<kBF16, true>(P, mode, B, s) : launch<kBF16, false>(P, mode, B, s);
-    return err == hipSuccess ? D3D_OK : (int)err;
+extern "C" int d3d_accept_fused_sparse(const void* target, int dtype, int input_kind,
+                                       const int64_t* draft_tokens, const int64_t* q_ids, const float* q_probs,
+                                       int S, const float* uniforms, const float* resample_u, float temperature,
+                                       int B, int K, int64_t V, int32_t* accepted, uint8_t* accept_mask,
+                                       int64_t* out_token, uint8_t* all_accepted, int64_t* posterior,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+    if (S < 1) return D3D_E_SHAPE;
+    return accept::run(target, nullptr, q_ids, q_probs, S, dtype, input_kind, draft_tokens, uniforms, resample_u,
+                       temperature, B, K, V, accepted, accept_mask, out_token, all_accepted, posterior, workspace,
+                       workspace_bytes, stream);
 }

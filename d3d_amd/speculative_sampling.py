@@ -12,8 +12,9 @@ are additions, not changes:
   ``resample_uniform``: token = first t with C_t > u * W over the (residual
   or bonus) weights, else the last t with positive weight.
 
-Batched entry points (``accept_fused``, ``greedy_accept``) take B requests
-in one launch; the reference functions keep the reference's B == 1 rule.
+Batched entry points (``accept_fused``, ``accept_fused_sparse``,
+``greedy_accept``) take B requests in one launch; the reference functions
+keep the reference's B == 1 rule.
 """
 from __future__ import annotations
 
@@ -48,6 +49,12 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     if t.dtype not in (torch.float32, torch.bfloat16):
         t = t.float()
     return t.contiguous()
+
+
+def _outputs(B: int, K: int, dev: torch.device):
+    return (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, K, dtype=torch.uint8, device=dev),
+            torch.empty(B, dtype=torch.int64, device=dev), torch.empty(B, dtype=torch.uint8, device=dev),
+            torch.empty(B, K + 1, dtype=torch.int64, device=dev))
 
 
 def accept_fused(
@@ -98,12 +105,7 @@ def accept_fused(
         draft = uniforms = resample_uniform = None
     tokens = draft_tokens.to(device=dev, dtype=torch.int64).contiguous()
 
-    accepted = torch.empty(B, dtype=torch.int32, device=dev)
-    mask = torch.empty(B, K, dtype=torch.uint8, device=dev)
-    out_token = torch.empty(B, dtype=torch.int64, device=dev)
-    all_acc = torch.empty(B, dtype=torch.uint8, device=dev)
-    posterior = torch.empty(B, K + 1, dtype=torch.int64, device=dev)
-
+    accepted, mask, out_token, all_acc, posterior = _outputs(B, K, dev)
     lib = _lib.load()
     nbytes = lib.d3d_accept_workspace_bytes(B, K, V)
     ws = _lib.workspace(dev, "accept", nbytes)
@@ -115,6 +117,65 @@ def accept_fused(
         _lib.ptr(posterior), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
     )
     _lib.check(status, "d3d_accept_fused")
+    return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), posterior)
+
+
+def accept_fused_sparse(
+    target: torch.Tensor,
+    draft_tokens: torch.Tensor,
+    draft_token_ids: torch.Tensor,
+    draft_token_probs: torch.Tensor,
+    *,
+    temperature: float = 1.0,
+    uniforms: Optional[torch.Tensor] = None,
+    resample_uniform: Optional[torch.Tensor] = None,
+    input_kind: str = "probs",
+    generator: Optional[torch.Generator] = None,
+) -> AcceptOutput:
+    """Batched fused acceptance against sparse proposals, one launch.
+
+    ``target`` [B, K+1, V] as in :func:`accept_fused`; the draft side is
+    ``draft_token_ids`` / ``draft_token_probs`` [B, K, S] (S <= 1024), the
+    proposal support of single/speculative_sampling.py:79-143.  Support ids
+    outside [0, V) carry no mass.  No host synchronisation.
+    """
+    if target.ndim != 3 or draft_tokens.ndim != 2:
+        raise ValueError("expected draft_tokens [B,K] and target [B,K+1,V]")
+    if draft_token_ids.ndim != 3 or draft_token_probs.ndim != 3:
+        raise ValueError("expected sparse draft ids/probs [B,K,S]")
+    B, K = draft_tokens.shape
+    if target.shape[0] != B or target.shape[1] != K + 1:
+        raise ValueError("target must contain K draft rows plus one bonus row")
+    if draft_token_ids.shape[:2] != (B, K):
+        raise ValueError("sparse draft support must contain one row per draft token")
+    if draft_token_probs.shape != draft_token_ids.shape:
+        raise ValueError("sparse draft ids and probs must have identical shapes")
+    V, S = target.shape[2], draft_token_ids.shape[2]
+    kind = {"logits": _lib.D3D_INPUT_LOGITS, "probs": _lib.D3D_INPUT_PROBS}.get(input_kind)
+    if kind is None:
+        raise ValueError(f"input_kind must be 'logits' or 'probs', got {input_kind!r}")
+    dev = _lib.require_device(target, draft_tokens, draft_token_ids, draft_token_probs)
+    target = _prep(target)
+    if uniforms is None:
+        uniforms = torch.rand(B, K, device=dev, generator=generator)
+    if resample_uniform is None:
+        resample_uniform = torch.rand(B, device=dev, generator=generator)
+    uniforms = uniforms.to(device=dev, dtype=torch.float32).reshape(B, K).contiguous()
+    resample_uniform = resample_uniform.to(device=dev, dtype=torch.float32).reshape(B).contiguous()
+    tokens = draft_tokens.to(device=dev, dtype=torch.int64).contiguous()
+    q_ids = draft_token_ids.to(dtype=torch.int64).contiguous()
+    q_probs = draft_token_probs.to(dtype=torch.float32).contiguous()
+
+    accepted, mask, out_token, all_acc, posterior = _outputs(B, K, dev)
+    lib = _lib.load()
+    ws = _lib.workspace(dev, "accept", lib.d3d_accept_workspace_bytes(B, K, V))
+    status = lib.d3d_accept_fused_sparse(
+        _lib.ptr(target), _lib.dtype_code(target), kind, _lib.ptr(tokens), _lib.ptr(q_ids), _lib.ptr(q_probs),
+        S, _lib.ptr(uniforms), _lib.ptr(resample_uniform), float(temperature), B, K, V,
+        _lib.ptr(accepted), _lib.ptr(mask), _lib.ptr(out_token), _lib.ptr(all_acc),
+        _lib.ptr(posterior), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
+    )
+    _lib.check(status, "d3d_accept_fused_sparse")
     return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), posterior)
 
 
@@ -164,6 +225,42 @@ def verify_speculative_block(
         target_probs, draft_probs, draft_tokens,
         uniforms=uniforms, resample_uniform=resample_uniform,
         input_kind="probs", generator=generator,
+    )
+    return _to_result(out)
+
+
+def verify_speculative_block_sparse(
+    draft_tokens: torch.Tensor,
+    target_probs: torch.Tensor,
+    draft_token_ids: torch.Tensor,
+    draft_token_probs: torch.Tensor,
+    *,
+    uniforms: Optional[torch.Tensor] = None,
+    resample_uniform: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+) -> SpeculativeSampleResult:
+    """Verify against an exact sparse proposal distribution.
+
+    single/speculative_sampling.py:79-143: ``draft_tokens`` [B, K],
+    ``target_probs`` [B, K+1, V], ``draft_token_ids`` / ``draft_token_probs``
+    [B, K, S]; B must be 1, as in the reference.
+    """
+    if draft_tokens.ndim != 2 or target_probs.ndim != 3:
+        raise ValueError("expected draft_tokens [B,K] and target_probs [B,K+1,V]")
+    if draft_token_ids.ndim != 3 or draft_token_probs.ndim != 3:
+        raise ValueError("expected sparse draft ids/probs [B,K,S]")
+    batch, draft_len = draft_tokens.shape
+    if batch != 1:
+        raise ValueError("standard verification currently supports batch size 1")
+    if target_probs.shape[:2] != (batch, draft_len + 1):
+        raise ValueError("target_probs must contain K draft rows plus one bonus row")
+    if draft_token_ids.shape[:2] != (batch, draft_len):
+        raise ValueError("sparse draft support must contain one row per draft token")
+    if draft_token_probs.shape != draft_token_ids.shape:
+        raise ValueError("sparse draft ids and probs must have identical shapes")
+    out = accept_fused_sparse(
+        target_probs, draft_tokens, draft_token_ids, draft_token_probs,
+        uniforms=uniforms, resample_uniform=resample_uniform, input_kind="probs", generator=generator,
     )
     return _to_result(out)
 

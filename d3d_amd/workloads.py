@@ -53,6 +53,34 @@ def accept_inputs(seed: int, B: int = 1, K: int = 15, V: int = VOCAB, temperatur
 
 
 @dataclass
+class SparseAcceptInputs:
+    target: torch.Tensor  # [B, K+1, V] fp32 logits
+    tokens: torch.Tensor  # [B, K] int64
+    q_ids: torch.Tensor  # [B, K, S] int64 support ids
+    q_probs: torch.Tensor  # [B, K, S] fp32 support probabilities
+    uniforms: torch.Tensor  # [B, K] fp32
+    resample_u: torch.Tensor  # [B] fp32
+
+
+def sparse_accept_inputs(seed: int, B: int = 1, K: int = 15, V: int = VOCAB, S: int = 64,
+                         temperature: float = 1.0, target_std: float = 2.0,
+                         noise_std: float = 0.5) -> SparseAcceptInputs:
+    """Sparse proposals as single/eval_sync.py:341-367 forms them: the
+    top-S draft logits at ``temperature``, softmax over that support, and
+    the draft token drawn from it (inverse CDF over a seeded uniform)."""
+    base = accept_inputs(seed, B, K, V, temperature=1.0, target_std=target_std, noise_std=noise_std)
+    g = torch.Generator().manual_seed(seed + 7919)
+    vals, ids = torch.topk(base.draft / max(temperature, 1e-5), k=S, dim=-1)
+    probs = torch.softmax(vals, dim=-1)
+    cdf = probs.double().cumsum(-1)
+    u = torch.rand(B, K, generator=g)
+    local = torch.searchsorted(cdf, (u.double() * cdf[..., -1])[..., None], right=True).clamp_(max=S - 1)
+    tokens = ids.gather(-1, local)[..., 0]
+    return SparseAcceptInputs(base.target, tokens.long(), ids.long(), probs.float(), base.uniforms,
+                              base.resample_u)
+
+
+@dataclass
 class PagedKV:
     k_cache: torch.Tensor  # [num_pages, page_size, Hkv, D] bf16
     v_cache: torch.Tensor

@@ -95,6 +95,30 @@ int d3d_accept_fused(const void* target, const void* draft, int dtype, int input
                      size_t workspace_bytes, void* stream);
 
 /*
+ * Fused acceptance against sparse proposals: as d3d_accept_fused, with the
+ * draft side given as S (id, probability) pairs per position.
+ *
+ * Replaces single/speculative_sampling.py:79-143
+ * (verify_speculative_block_sparse), batched over B requests:
+ *   q_i(x)  = sum over s with q_ids[b,i,s] == x of q_probs[b,i,s] / Z_i,
+ *             Z_i = max(sum_s q_probs[b,i,s], 1e-12)
+ *   residual at the first reject j: p_j minus every q_probs[b,j,s] / Z_j at
+ *   q_ids[b,j,s] (subtracted in support order, duplicates accumulate), then
+ *   clamped at zero; p_j itself when that mass is <= 1e-12.
+ *
+ * q_ids [B, K, S] int64 (ids outside [0, V) carry no mass), q_probs
+ * [B, K, S] fp32, 1 <= S <= 1024.  Uses d3d_accept_workspace_bytes.  In
+ * greedy mode (logits, temperature <= 1e-5) the proposals are unused and
+ * the result is d3d_accept_fused's greedy acceptance.
+ */
+int d3d_accept_fused_sparse(const void* target, int dtype, int input_kind,
+                            const int64_t* draft_tokens, const int64_t* q_ids, const float* q_probs,
+                            int S, const float* uniforms, const float* resample_u, float temperature,
+                            int B, int K, int64_t V, int32_t* accepted, uint8_t* accept_mask,
+                            int64_t* out_token, uint8_t* all_accepted, int64_t* posterior,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Bytes of workspace the paged attention entry points need (split-context
  * partials).  max_context bounds every context_lens[b]; the same value must
  * be passed to the attention call.
