@@ -305,6 +305,7 @@ def main():
             "verify_ms": round(res["verify_ms"], 3),
             "draft_ms": round(res["draft_ms"], 3),
             "overlap_fraction": round(res["overlap_fraction"], 3),
+            "timeline_ms": res["timeline"][:3],
             "steps": res["steps"],
             "new_tokens": args.e2e_new_tokens,
             "batch": 4,

@@ -49,12 +49,18 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P],
     ),
+    "d3d_packed_block_attn": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _SZ, _P],
+    ),
     "d3d_kv_append": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _P]),
     "d3d_confidence_workspace_bytes": (_SZ, [_I, _I, _I64]),
     "d3d_confidence_topk_unmask": (
         _I,
         [_P, _I, _P, _I64, _I, _F, _I, _I, _I64, _P, _P, _P, _SZ, _P],
     ),
+    "d3d_topk_workspace_bytes": (_SZ, [_I, _I64, _I]),
+    "d3d_topk_rows": (_I, [_P, _I, _I, _I64, _I, _P, _P, _P, _SZ, _P]),
     "d3d_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "d3d_qk_rope_append": (
         _I,

@@ -19,7 +19,7 @@ All tensors live on one HIP device; there is no CPU path.
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Sequence, Optional
 
 import torch
 
@@ -59,8 +59,9 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: 
     _lib.check(st, "d3d_kv_append")
 
 
-def _attn(fn_name: str, q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, max_seqlen_k, out):
-    dev = _lib.require_device(q, k_cache, v_cache, cache_seqlens, block_table)
+def _attn(fn_name: str, q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale, max_seqlen_k, out,
+          vis=None):
+    dev = _lib.require_device(q, k_cache, v_cache, cache_seqlens, block_table, vis)
     _check_cache(k_cache, v_cache)
     if q.ndim != 4:
         raise ValueError("expected q [B, Q, Hq, D]")
@@ -84,8 +85,9 @@ def _attn(fn_name: str, q, k_cache, v_cache, cache_seqlens, block_table, softmax
     lib = _lib.load()
     nbytes = lib.d3d_attn_workspace_bytes(B, Q, Hq, Hkv, D, ps, int(max_seqlen_k))
     ws = _lib.workspace(dev, "attn", nbytes)
+    vis_args = () if vis is None else (vis.data_ptr(),)
     st = getattr(lib, fn_name)(
-        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(),
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), bt.data_ptr(), lens.data_ptr(), *vis_args,
         out.data_ptr(), B, Q, Hq, Hkv, D, ps, max_pages, P, float(scale), int(max_seqlen_k),
         ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     _lib.check(st, fn_name)
@@ -116,3 +118,37 @@ def draft_block_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     """Draft block attention: prefix plus a bidirectional block (recovery mask)."""
     return _attn("d3d_draft_block_attn", q, k_cache, v_cache, context_lens, block_table,
                  softmax_scale, max_seqlen_k, out)
+
+
+def packed_visibility(K: int, accepted: Sequence[int]) -> torch.Tensor:
+    """Per-query visibility [Q, 3] int32 of a packed draft block (CPU tensor).
+
+    Rows 0..K-1 are the pending block, causal over prefix + block
+    (serving/engine.py:45); branch j (rows K + jK ..) has ``accepted[j]``
+    accepted pending tokens and sees the prefix, those tokens and its own K
+    positions bidirectionally (serving/engine.py:46-50).  Q = K (1 + len(accepted)).
+    """
+    rows = [(i + 1, 0, 0) for i in range(K)]
+    for j, n in enumerate(accepted):
+        if not 0 <= n <= K:
+            raise ValueError("accepted counts must lie in [0, K]")
+        off = K + j * K
+        rows.extend((n, off, off + K) for _ in range(K))
+    return torch.tensor(rows, dtype=torch.int32)
+
+
+def packed_block_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, context_lens: torch.Tensor,
+                      block_table: torch.Tensor, q_visibility: torch.Tensor, *,
+                      softmax_scale: Optional[float] = None, max_seqlen_k: Optional[int] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Packed multi-branch draft attention over a paged cache.
+
+    ``q`` [B, Q, Hq, D]; ``context_lens`` = prefix + Q (the packed block's
+    keys are appended after the prefix); ``q_visibility`` [Q, 3] int32 on
+    the device: query i sees keys t < prefix + v[i, 0] and
+    prefix + v[i, 1] <= t < prefix + v[i, 2] (see :func:`packed_visibility`).
+    """
+    if q_visibility.shape != (q.shape[1], 3) or q_visibility.dtype != torch.int32:
+        raise ValueError("q_visibility must be int32 [Q, 3]")
+    return _attn("d3d_packed_block_attn", q, k_cache, v_cache, context_lens, block_table, softmax_scale,
+                 max_seqlen_k, out, vis=q_visibility.contiguous())

@@ -11,15 +11,23 @@
 //       draft recovery: every block query sees keys j < ctx (prefix + block)
 //   models/d3d/modeling_d3d.py:190-200             GQA: head h reads KV head
 //       h / (Hq / Hkv)
+//   serving/engine.py:35-52 with :73-131           packed multi-branch draft:
+//       the pending block (causal over prefix + block) followed by branch
+//       blocks that see the prefix, the first n pending tokens and their
+//       own block (bidirectional); here a per-query descriptor replaces the
+//       materialised [B, 1, Q, S] bool mask
 //
 // Layouts (bf16): q and out [B, Q, Hq, D]; caches [num_pages, page, Hkv, D]
 // (the reference's layout, serving/backend.py:46-48); block_table
 // [B, max_pages] int32; context_lens [B] int32 = prefix + Q (the block's own
 // keys are already appended).
 //
-// Work decomposition: workgroup (split, kv_head, b).  The G = Hq/Hkv query
-// heads of the group times the Q block queries form the MFMA rows (row
-// r = g*Q + qi, 16 rows per wave).  Each workgroup walks its split of the
+// Work decomposition: workgroup (split, kv_head, b * query tiles + tile).
+// The G = Hq/Hkv query heads of the group times QT queries of the block
+// form the MFMA rows (row r = g*QT + qi, 16 rows per wave, at most 128).
+// Key t is visible to a row iff t < A or S_lo <= t < S_hi (two ranges):
+// causal A = ctx - Q + qi + 1; bidirectional A = ctx; packed A = prefix +
+// vis[qi][0], [S_lo, S_hi) = prefix + [vis[qi][1], vis[qi][2]).  Each workgroup walks its split of the
 // context in 64-token tiles staged in LDS; all waves share a tile.  Scores
 // are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16: the
 // result layout (lane l holds tokens 4*(l/16)+r of row l%16) is, two 16-token
@@ -62,8 +70,12 @@ struct Params {
     int page_size, max_pages, num_pages;
     int page_shift;  // log2(page_size) for powers of two, else -1
     int split_tokens, num_splits;
-    float scale_log2;  // softmax scale * log2(e)
+    int QT, nqt;        // queries per workgroup, query tiles per request
+    const int32_t* vis; // packed mode: [Q][3] visibility descriptor
+    float scale_log2;   // softmax scale * log2(e)
 };
+
+enum : int { kCausal = 0, kFull = 1, kPacked = 2 };
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -127,19 +139,65 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
 
 // Register budget: two workgroups per CU (two waves per SIMD) so that each
 // CU keeps 2 x DEPTH tiles of K/V in flight.
-template <int NW, bool CAUSAL>
+template <int NW, int MODE>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
     constexpr int NT = NW * 64;
-    const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int s = blockIdx.x, kvh = blockIdx.y;
+    const int b = blockIdx.z / P.nqt, qt = blockIdx.z - b * P.nqt;
+    const int q0 = qt * P.QT;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g4 = lane >> 4, c16 = lane & 15;
 
     __shared__ __attribute__((aligned(16))) char lds[2 * TILE * ROWB];
     __shared__ int pages[kMaxSplitPages];
+    __shared__ int s_lim[2][NW];
 
     const int ctx = min(P.context_lens[b], P.max_pages * P.page_size);
+
+    // This lane's query row for the Q^T operand and the softmax statistics.
+    const int row = w * 16 + c16;
+    const int gh = row / P.QT, qi = q0 + (row - gh * P.QT);
+    const bool row_ok = row < P.M && qi < P.Q;
+    const int head = kvh * P.G + (row_ok ? gh : 0);
+    // Visible keys: t < va, or vlo <= t < vhi.
+    int va = 0, vlo = 0, vhi = 0;
+    if (row_ok) {
+        if constexpr (MODE == kCausal) {
+            va = ctx - P.Q + qi + 1;
+        } else if constexpr (MODE == kFull) {
+            va = ctx;
+        } else {
+            const int pre = ctx - P.Q;
+            va = pre + P.vis[qi * 3 + 0];
+            vlo = pre + P.vis[qi * 3 + 1];
+            vhi = pre + P.vis[qi * 3 + 2];
+        }
+        va = min(va, ctx);
+        vhi = min(vhi, ctx);
+    }
+    // Workgroup bounds: keys below a_min are visible to every row; none at
+    // or past w_end is visible to any.
+    {
+        int amin = row_ok ? va : INT_MAX, wend = row_ok ? max(va, vhi) : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            amin = min(amin, __shfl_xor(amin, o, 64));
+            wend = max(wend, __shfl_xor(wend, o, 64));
+        }
+        if (lane == 0) {
+            s_lim[0][w] = amin;
+            s_lim[1][w] = wend;
+        }
+    }
+    __syncthreads();
+    int a_min = INT_MAX, w_end = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        a_min = min(a_min, s_lim[0][i]);
+        w_end = max(w_end, s_lim[1][i]);
+    }
     const int t_begin = s * P.split_tokens;
-    const int t_end = min(t_begin + P.split_tokens, ctx);
+    const int t_end = min(min(t_begin + P.split_tokens, ctx), w_end);
     // Page ids of the whole split in one round trip (split starts are page aligned).
     const int p0 = t_begin / P.page_size;
     const int np = t_end > t_begin ? (t_end - 1) / P.page_size - p0 + 1 : 0;
@@ -154,15 +212,6 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             break;
         }
 
-    // This lane's query row for the Q^T operand and the softmax statistics.
-    const int row = w * 16 + c16;
-    const bool row_ok = row < P.M;
-    const int gh = row_ok ? row / P.Q : 0, qi = row_ok ? row % P.Q : 0;
-    const int head = kvh * P.G + gh;
-    // Largest key index this row may see.
-    const int limit = !row_ok ? -1 : (CAUSAL ? ctx - P.Q + qi : ctx - 1);
-    // Keys at or below limit_min are visible to every row of the workgroup.
-    const int limit_min = CAUSAL ? ctx - P.Q : ctx - 1;
 
     // Q^T operand of v_mfma_f32_16x16x32_bf16: lane l holds row l%16, head
     // dims 32*ks + 8*(l/16) + 0..7.  K is read with the same dim assignment,
@@ -208,15 +257,16 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
 #pragma unroll
                 for (int r = 0; r < 4; ++r) sc[m][r] = acc[m][r] * P.scale_log2;
         }
-        // Masking only where the tile crosses the split end or the causal
-        // frontier of the earliest query (a uniform test).
-        if (t0 + TILE > min(t_end, limit_min + 1)) {
+        // Masking only where the tile crosses the split end or the
+        // visibility frontier of some row (a uniform test).
+        if (t0 + TILE > min(t_end, a_min)) {
 #pragma unroll
             for (int m = 0; m < TILE / 16; ++m)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = t0 + 16 * m + 4 * g4 + r;
-                    if (!(t <= limit && t < t_end)) sc[m][r] = -INFINITY;
+                    const bool vis = t < va || (MODE == kPacked && t >= vlo && t < vhi);
+                    if (!(vis && t < t_end)) sc[m][r] = -INFINITY;
                 }
         }
         float tmax = -INFINITY;
@@ -332,8 +382,8 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         for (int r = 0; r < 4; ++r) {
             const int orow = w * 16 + 4 * g4 + r;
             const float sc_r = __shfl(inv, 4 * g4 + r, 64);
-            if (orow < P.M) {
-                const int oh = kvh * P.G + orow / P.Q, oq = orow % P.Q;
+            const int oh = kvh * P.G + orow / P.QT, oq = q0 + orow % P.QT;
+            if (orow < P.M && oq < P.Q) {
                 uint16_t* dst = P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D;
 #pragma unroll
                 for (int h = 0; h < D / 64; ++h) {
@@ -344,7 +394,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             }
         }
     } else {
-        const size_t unit = ((size_t)b * P.Hkv + kvh) * P.num_splits + s;
+        const size_t unit = ((size_t)blockIdx.z * P.Hkv + kvh) * P.num_splits + s;
         float* po = P.part_o + unit * P.M * D;
         float* pml = P.part_ml + unit * P.M * 2;
 #pragma unroll
@@ -372,9 +422,10 @@ constexpr int kRowsPerCombine = 8;
 constexpr int kMaxSplits = 256;
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
-    const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y, b = blockIdx.z;
+    const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y;
+    const int b = blockIdx.z / P.nqt, q0 = (blockIdx.z - b * P.nqt) * P.QT;
     const int S = P.num_splits;
-    const size_t unit0 = ((size_t)b * P.Hkv + kvh) * S;
+    const size_t unit0 = ((size_t)blockIdx.z * P.Hkv + kvh) * S;
     __shared__ float wts[kRowsPerCombine][kMaxSplits];
     __shared__ float lsum[kRowsPerCombine][kMaxSplits];
     __shared__ float inv_den[kRowsPerCombine];
@@ -411,7 +462,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     }
     __syncthreads();
     const int rr = threadIdx.x / 32, c4 = (threadIdx.x % 32) * 4, row = r0 + rr;
-    if (row >= P.M) return;
+    const int oh = kvh * P.G + row / P.QT, oq = q0 + row % P.QT;
+    if (row >= P.M || oq >= P.Q) return;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
     for (int sp = 0; sp < S; ++sp) {
@@ -420,7 +472,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
         acc += w * o;
     }
     const float sc = inv_den[rr];
-    const int oh = kvh * P.G + row / P.Q, oq = row % P.Q;
     const u32x2 v = {pack_bf16x2(acc[0] * sc, acc[1] * sc), pack_bf16x2(acc[2] * sc, acc[3] * sc)};
     *reinterpret_cast<u32x2*>(P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D + c4) = v;
 }
@@ -442,7 +493,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* k, const
 }
 
 struct Plan {
-    int waves, split_tokens, num_splits;
+    int waves, split_tokens, num_splits, QT, nqt;
     bool valid;
     size_t part_o_bytes, part_ml_bytes, total;
 };
@@ -457,10 +508,13 @@ constexpr int kTargetWorkgroups = 1024;
 
 static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
     Plan p;
-    const int M = (Hq / Hkv) * Q;
+    const int G = Hq / Hkv;
+    p.QT = Q < kMaxWaves * 16 / G ? Q : kMaxWaves * 16 / G;
+    p.nqt = (Q + p.QT - 1) / p.QT;
+    const int M = G * p.QT;
     p.waves = M <= 32 ? 2 : (M <= 64 ? 4 : 8);
     const int tiles = (max_context + TILE - 1) / TILE;
-    const int units = B * Hkv;
+    const int units = B * p.nqt * Hkv;
     int splits = (kTargetWorkgroups + units - 1) / units;
     splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
     splits = splits > kMaxSplits ? kMaxSplits : splits;
@@ -477,8 +531,8 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
     if (p.num_splits == 1) {
         p.part_o_bytes = p.part_ml_bytes = 0;
     } else {
-        p.part_o_bytes = align256((size_t)B * Hkv * p.num_splits * M * D * sizeof(float));
-        p.part_ml_bytes = align256((size_t)B * Hkv * p.num_splits * M * 2 * sizeof(float));
+        p.part_o_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * D * sizeof(float));
+        p.part_ml_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * 2 * sizeof(float));
     }
     p.total = p.part_o_bytes + p.part_ml_bytes;
     if (p.total == 0) p.total = 256;
@@ -489,22 +543,25 @@ static int validate(int B, int Q, int Hq, int Hkv, int D_, int page_size, int ma
                     int max_context) {
     if (B < 1 || B > 65535 || Q < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv) return D3D_E_SHAPE;
     if (D_ != D) return D3D_E_UNSUPPORTED;
-    if ((Hq / Hkv) * Q > kMaxWaves * 16) return D3D_E_UNSUPPORTED;
+    if (Hq / Hkv > kMaxWaves * 16) return D3D_E_UNSUPPORTED;
+    if ((int64_t)B * ((Q + 127) / 128) * (Hq / Hkv) > 65535 * 128) return D3D_E_SHAPE;
     if (page_size < 1 || max_pages < 1 || num_pages < 1 || max_context < 1) return D3D_E_SHAPE;
     if ((int64_t)max_pages * page_size < max_context) return D3D_E_SHAPE;
     return D3D_OK;
 }
 
-template <bool CAUSAL>
+template <int MODE>
 static int run(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
-               const int32_t* context_lens, void* out, int B, int Q, int Hq, int Hkv, int D_, int page_size,
-               int max_pages, int num_pages, float scale, int max_context, void* workspace, size_t ws_bytes,
-               void* stream) {
+               const int32_t* context_lens, const int32_t* vis, void* out, int B, int Q, int Hq, int Hkv, int D_,
+               int page_size, int max_pages, int num_pages, float scale, int max_context, void* workspace,
+               size_t ws_bytes, void* stream) {
     const int st = validate(B, Q, Hq, Hkv, D_, page_size, max_pages, num_pages, max_context);
     if (st != D3D_OK) return st;
     if (!q || !k_cache || !v_cache || !block_table || !context_lens || !out) return D3D_E_NULL;
+    if (MODE == kPacked && !vis) return D3D_E_NULL;
     const Plan pl = plan(B, Q, Hq, Hkv, max_context, page_size);
     if (!pl.valid) return D3D_E_UNSUPPORTED;
+    if ((int64_t)B * pl.nqt > 65535) return D3D_E_SHAPE;
     if (pl.num_splits > 1 && (!workspace || ws_bytes < pl.total)) return D3D_E_WORKSPACE;
     Params P;
     P.q = static_cast<const uint16_t*>(q);
@@ -521,7 +578,10 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     P.Hq = Hq;
     P.Hkv = Hkv;
     P.G = Hq / Hkv;
-    P.M = P.G * Q;
+    P.QT = pl.QT;
+    P.nqt = pl.nqt;
+    P.M = P.G * pl.QT;
+    P.vis = vis;
     P.page_size = page_size;
     P.page_shift = -1;
     if ((page_size & (page_size - 1)) == 0) {
@@ -535,21 +595,22 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     P.num_splits = pl.num_splits;
     P.scale_log2 = scale * 1.4426950408889634f;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(pl.num_splits, Hkv, B);
+    const dim3 grid(pl.num_splits, Hkv, B * pl.nqt);
     switch (pl.waves) {
         case 2:
-            hipLaunchKernelGGL((attn_split_kernel<2, CAUSAL>), grid, dim3(128), 0, s, P);
+            hipLaunchKernelGGL((attn_split_kernel<2, MODE>), grid, dim3(128), 0, s, P);
             break;
         case 4:
-            hipLaunchKernelGGL((attn_split_kernel<4, CAUSAL>), grid, dim3(256), 0, s, P);
+            hipLaunchKernelGGL((attn_split_kernel<4, MODE>), grid, dim3(256), 0, s, P);
             break;
         default:
-            hipLaunchKernelGGL((attn_split_kernel<8, CAUSAL>), grid, dim3(512), 0, s, P);
+            hipLaunchKernelGGL((attn_split_kernel<8, MODE>), grid, dim3(512), 0, s, P);
             break;
     }
     if (pl.num_splits > 1)
-        hipLaunchKernelGGL(attn_combine_kernel, dim3((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B),
-                           dim3(256), 0, s, P);
+        hipLaunchKernelGGL(attn_combine_kernel,
+                           dim3((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B * pl.nqt), dim3(256), 0, s,
+                           P);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }
@@ -571,8 +632,9 @@ extern "C" int d3d_verify_attn_paged(const void* q, const void* k_cache, const v
                                      int Q, int Hq, int Hkv, int D, int page_size, int max_pages, int num_pages,
                                      float scale, int max_context, void* workspace, size_t workspace_bytes,
                                      void* stream) {
-    return attn::run<true>(q, k_cache, v_cache, block_table, context_lens, out, B, Q, Hq, Hkv, D, page_size,
-                           max_pages, num_pages, scale, max_context, workspace, workspace_bytes, stream);
+    return attn::run<attn::kCausal>(q, k_cache, v_cache, block_table, context_lens, nullptr, out, B, Q, Hq, Hkv, D,
+                                    page_size, max_pages, num_pages, scale, max_context, workspace,
+                                    workspace_bytes, stream);
 }
 
 extern "C" int d3d_draft_block_attn(const void* q, const void* k_cache, const void* v_cache,
@@ -580,8 +642,19 @@ extern "C" int d3d_draft_block_attn(const void* q, const void* k_cache, const vo
                                     int Q, int Hq, int Hkv, int D, int page_size, int max_pages, int num_pages,
                                     float scale, int max_context, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-    return attn::run<false>(q, k_cache, v_cache, block_table, context_lens, out, B, Q, Hq, Hkv, D, page_size,
-                            max_pages, num_pages, scale, max_context, workspace, workspace_bytes, stream);
+    return attn::run<attn::kFull>(q, k_cache, v_cache, block_table, context_lens, nullptr, out, B, Q, Hq, Hkv, D,
+                                  page_size, max_pages, num_pages, scale, max_context, workspace, workspace_bytes,
+                                  stream);
+}
+
+extern "C" int d3d_packed_block_attn(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_table, const int32_t* context_lens,
+                                     const int32_t* q_visibility, void* out, int B, int Q, int Hq, int Hkv, int D,
+                                     int page_size, int max_pages, int num_pages, float scale, int max_context,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+    return attn::run<attn::kPacked>(q, k_cache, v_cache, block_table, context_lens, q_visibility, out, B, Q, Hq,
+                                    Hkv, D, page_size, max_pages, num_pages, scale, max_context, workspace,
+                                    workspace_bytes, stream);
 }
 
 extern "C" int d3d_kv_append(const void* k, const void* v, void* k_cache, void* v_cache,

@@ -60,6 +60,29 @@ def confidence_topk_unmask(logits: torch.Tensor, block: torch.Tensor, mask_id: i
     return x0, conf
 
 
+def topk_tokens(logits: torch.Tensor, k: int, with_values: bool = False):
+    """Top-k token ids [..., k] int64 of logits [..., V] (fp32 or bf16), one launch pair.
+
+    Descending value, equal values by ascending id: ``ids[..., 0]`` is the
+    argmax (torch's first maximum).  serving/backend.py:84-93 (greedy and
+    ``logits.topk(k).indices``).  With ``with_values`` also returns the
+    values [..., k] fp32.
+    """
+    dev = _lib.require_device(logits)
+    lg = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
+    lg = lg.contiguous()
+    V = lg.shape[-1]
+    N = lg.numel() // V
+    ids = torch.empty(*lg.shape[:-1], k, dtype=torch.int64, device=dev)
+    vals = torch.empty(*lg.shape[:-1], k, dtype=torch.float32, device=dev) if with_values else None
+    lib = _lib.load()
+    ws = _lib.workspace(dev, "topk", lib.d3d_topk_workspace_bytes(max(N, 1), V, k))
+    st = lib.d3d_topk_rows(lg.data_ptr(), _lib.dtype_code(lg), N, V, int(k), ids.data_ptr(), _lib.ptr(vals),
+                           ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_topk_rows")
+    return (ids, vals) if with_values else ids
+
+
 def draft_block_forward(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], ids: torch.Tensor,
                         name: str = "draft", starts: Optional[List[int]] = None) -> torch.Tensor:
     """Logits [B, Q, V] of a block at positions starts[b].. (prefix + bidirectional block)."""

@@ -122,11 +122,14 @@ class Qwen3PagedModel(torch.nn.Module):
 
     def forward(self, ids: torch.Tensor, positions: torch.Tensor, kv: PagedKV, block_tables: torch.Tensor,
                 context_lens: torch.Tensor, slot_mapping: torch.Tensor, *, causal: bool,
-                max_context: int) -> torch.Tensor:
+                max_context: int, q_vis: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Hidden states [B, Q, hidden] of a block of Q tokens per request.
 
         The block's K/V are appended at ``slot_mapping`` before attention;
-        ``context_lens`` counts the prefix plus the block.  Per layer: fused
+        ``context_lens`` counts the prefix plus the block.  With ``q_vis``
+        ([Q, 3] int32, device) the block is a packed multi-branch draft block
+        and attention follows that per-query visibility; otherwise it is
+        causal (verify) or bidirectional (draft recovery) within the block.  Per layer: fused
         add + RMSNorm, QKV GEMM, fused q/k norm + RoPE + KV append, paged
         attention, O GEMM, fused add + RMSNorm, gate-up GEMM, fused SiLU-mul,
         down GEMM (the decoder layer of serving/vendor/ssd/models/qwen3.py).
@@ -143,8 +146,12 @@ class Qwen3PagedModel(torch.nn.Module):
             qkv = F.linear(hs, L["qkv"])
             q = ly.qk_rope_append(qkv, pos, L["qn"], L["kn"], self.inv_freq, kv.k[li], kv.v[li], slot_mapping,
                                   Hq, Hkv, s.eps, draft_rope=self.draft)
-            o = att.flash_attn_with_kvcache(q.view(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens,
-                                            block_tables, causal=causal, max_seqlen_k=max_context)
+            if q_vis is None:
+                o = att.flash_attn_with_kvcache(q.view(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens,
+                                                block_tables, causal=causal, max_seqlen_k=max_context)
+            else:
+                o = att.packed_block_attn(q.view(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens, block_tables,
+                                          q_vis, max_seqlen_k=max_context)
             x = F.linear(o.reshape(B * Q, Hq * d), L["o"])
             ly.add_rmsnorm(x, residual, L["ln2"], s.eps, out=hs)
             x = F.linear(ly.silu_mul(F.linear(hs, L["gate_up"])), L["down"])
@@ -230,9 +237,10 @@ class BlockStep:
     """
 
     def __init__(self, model: "Qwen3PagedModel", kv: PagedKV, B: int, Q: int, width: int, causal: bool,
-                 post=None, use_graph: bool = True):
+                 post=None, use_graph: bool = True, q_vis: Optional[torch.Tensor] = None):
         dev = model.device
         self.model, self.kv, self.causal, self.post, self.use_graph = model, kv, causal, post, use_graph
+        self.q_vis = None if q_vis is None else q_vis.to(dev, torch.int32).contiguous()
         self.ids = torch.zeros(B, Q, dtype=torch.int64, device=dev)
         self.pos = torch.zeros(B, Q, dtype=torch.int64, device=dev)
         self.tables = torch.zeros(B, width, dtype=torch.int32, device=dev)
@@ -245,7 +253,7 @@ class BlockStep:
 
     def _body(self):
         hidden = self.model(self.ids, self.pos, self.kv, self.tables, self.lens, self.slots, causal=self.causal,
-                            max_context=self.max_ctx)
+                            max_context=self.max_ctx, q_vis=self.q_vis)
         return self.post(hidden, self.ids) if self.post is not None else None
 
     def _load(self, ids, pos, tables, slots, lens):

@@ -1,7 +1,9 @@
 /*
  * libd3d_hip -- C ABI of the MI355X (gfx950) kernels for D3D's per-step
  * speculative hot path: fused acceptance, paged block-verify attention,
- * KV append, diffusion-draft block attention and confidence/top-k unmask.
+ * KV append, diffusion-draft block attention (recovery and packed
+ * multi-branch), confidence/top-k unmask and the fused per-layer glue of the
+ * target and draft forwards.
  *
  * Conventions shared by every entry point:
  *  - All tensor arguments are device pointers to contiguous row-major data
@@ -140,7 +142,8 @@ size_t d3d_attn_workspace_bytes(int B, int Q, int Hq, int Hkv, int D, int page_s
  * context_lens [B] int32, keys per request including the block's own Q
  *              keys (already appended); query i sees keys
  *              j <= context_lens[b] - Q + i
- * D must be 128; (Hq / Hkv) * Q <= 128.  Page ids outside [0, num_pages)
+ * D must be 128; Hq / Hkv <= 128 (blocks of more than 128 / (Hq / Hkv)
+ * queries are tiled over workgroups).  Page ids outside [0, num_pages)
  * read as zero keys/values instead of faulting.
  */
 int d3d_verify_attn_paged(const void* q, const void* k_cache, const void* v_cache,
@@ -164,6 +167,28 @@ int d3d_draft_block_attn(const void* q, const void* k_cache, const void* v_cache
                          int B, int Q, int Hq, int Hkv, int D, int page_size, int max_pages,
                          int num_pages, float scale, int max_context, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/*
+ * Packed multi-branch draft attention: as d3d_draft_block_attn, with the
+ * visible keys of each query given by a descriptor instead of a mask.
+ * With prefix = context_lens[b] - Q (the block's Q keys are appended after
+ * the prefix), query i sees key t iff
+ *     t < prefix + q_visibility[i][0]
+ *  or prefix + q_visibility[i][1] <= t < prefix + q_visibility[i][2].
+ * q_visibility [Q][3] int32 is shared by the B requests.  Q is unbounded
+ * (queries are tiled over workgroups).
+ *
+ * Replaces the draft branch of serving/vendor/ssd/layers/attention.py:42-52
+ * under the packed mask of serving/engine.py:43-50 (Engine._mask with
+ * branch specs): the pending block's rows i see (prefix + i + 1) keys,
+ * i.e. {i + 1, 0, 0}; rows of the branch at offset off with n accepted
+ * pending tokens see {n, off, off + K}.  Uses d3d_attn_workspace_bytes.
+ */
+int d3d_packed_block_attn(const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_table, const int32_t* context_lens,
+                          const int32_t* q_visibility, void* out, int B, int Q, int Hq, int Hkv,
+                          int D, int page_size, int max_pages, int num_pages, float scale,
+                          int max_context, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * KV append: k_cache.view(-1, Hkv, D)[slot_mapping] = k (and v), as at
@@ -196,6 +221,23 @@ int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids
                                int k, float temperature, int B, int Q, int64_t V, int64_t* x0_out,
                                float* conf_out, void* workspace, size_t workspace_bytes,
                                void* stream);
+
+/* Bytes of workspace d3d_topk_rows needs. */
+size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
+
+/*
+ * Top-k token ids of N logits rows [N, V] (fp32 or bf16): ids_out [N, k]
+ * int64 in descending order of value, equal values by ascending id (so
+ * ids_out[n][0] is the argmax with torch's first-maximum rule); NaN entries
+ * are never selected.  vals_out [N, k] fp32 may be NULL.  1 <= k <= 16,
+ * N <= 65535, ceil(V / 4096) * k <= 8192.
+ *
+ * Replaces logits.argmax(-1) and logits.topk(k).indices in Runner._run,
+ * serving/backend.py:84-93, which feed the anchor choice of
+ * Engine._recover / Engine._predict (serving/engine.py:54-131).
+ */
+int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int64_t* ids_out,
+                  float* vals_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Residual add + RMSNorm over rows of H bf16 entries (H a multiple of 8,

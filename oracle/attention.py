@@ -9,6 +9,8 @@ fp64 numpy restatement of the paged attention the reference runs:
   serving/engine.py:41-42 -- every block query sees keys j < ctx;
 * GQA: head h reads KV head h // (Hq / Hkv) (repeat_interleave at :47-48,
   repeat_kv at models/d3d/modeling_d3d.py:190-200);
+* packed multi-branch draft: the bool mask Engine._mask builds from branch
+  specs (serving/engine.py:35-52), restated by ``engine_mask``;
 * keys are gathered through the page table: token t of request b lives in
   page block_table[b, t // page_size] at offset t % page_size
   (serving/backend.py:123-124).
@@ -26,8 +28,33 @@ def gather_kv(cache: np.ndarray, block_table: np.ndarray, b: int, ctx: int) -> n
     return cache[pages, t % ps]
 
 
-def paged_attention(q, k_cache, v_cache, block_table, context_lens, scale, causal=True):
-    """q [B,Q,Hq,D]; caches [P,ps,Hkv,D]; returns fp64 [B,Q,Hq,D]."""
+def engine_mask(prefix: int, Q: int, S: int, K: int, specs=None) -> np.ndarray:
+    """[Q, S] bool mask of Engine._mask (serving/engine.py:35-52) for one request.
+
+    ``specs`` None is the recovery mask (every query sees cols < prefix + Q);
+    otherwise rows 0..K-1 see the prefix and the pending block causally, and
+    branch j (rows K + jK ..) with ``specs[j] = (accepted, anchor)`` sees
+    cols < prefix + accepted and its own K columns.
+    """
+    cols = np.arange(S)[None, :]
+    local = cols - prefix
+    if specs is None:
+        return np.broadcast_to(cols < prefix + Q, (Q, S)).copy()
+    mask = np.zeros((Q, S), bool)
+    rows = np.arange(K)[:, None]
+    mask[:K] = (cols < prefix) | ((local >= 0) & (local <= rows))
+    for j, (accepted, _anchor) in enumerate(specs):
+        off = K + j * K
+        mask[off:off + K] = (cols < prefix + accepted) | ((local >= off) & (local < off + K))
+    return mask
+
+
+def paged_attention(q, k_cache, v_cache, block_table, context_lens, scale, causal=True, masks=None):
+    """q [B,Q,Hq,D]; caches [P,ps,Hkv,D]; returns fp64 [B,Q,Hq,D].
+
+    ``masks`` (optional): per request a [Q, >= ctx] bool mask of visible keys,
+    overriding ``causal``.  Rows that see no key give zeros.
+    """
     q = np.asarray(q, np.float64)
     kc = np.asarray(k_cache, np.float64)
     vc = np.asarray(v_cache, np.float64)
@@ -42,12 +69,16 @@ def paged_attention(q, k_cache, v_cache, block_table, context_lens, scale, causa
         V = gather_kv(vc, bt, b, ctx)
         j = np.arange(ctx)[None, :]
         i = np.arange(Q)[:, None]
-        visible = (j <= ctx - Q + i) if causal else np.ones((Q, ctx), bool)
+        if masks is not None:
+            visible = np.asarray(masks[b])[:, :ctx]
+        else:
+            visible = (j <= ctx - Q + i) if causal else np.ones((Q, ctx), bool)
+        any_row = visible.any(axis=1, keepdims=True)
         for h in range(Hq):
             s = q[b, :, h, :] @ K[:, h // G, :].T * scale
             s = np.where(visible, s, -np.inf)
-            s -= s.max(axis=1, keepdims=True)
+            s -= np.where(any_row, s.max(axis=1, keepdims=True), 0.0)
             p = np.exp(s)
-            p /= p.sum(axis=1, keepdims=True)
+            p /= np.where(any_row, p.sum(axis=1, keepdims=True), 1.0)
             out[b, :, h, :] = p @ V[:, h // G, :]
     return out

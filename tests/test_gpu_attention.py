@@ -125,3 +125,54 @@ def test_kv_append_bit_exact_and_skips_negative_slots():
     att.kv_append(k, v, kc, vc, slots.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(kc, ek) and torch.equal(vc, ev)
+
+
+# -- query tiling and the packed multi-branch draft block -------------------
+@pytest.mark.parametrize("lens,Q,Hq,causal", [([700, 129], 64, 32, True), ([300], 100, 16, False),
+                                              ([2000 + 40], 40, 32, True)])
+def test_query_tiling_beyond_128_rows(lens, Q, Hq, causal):
+    """Blocks with (Hq/Hkv) * Q > 128 rows are tiled over workgroups."""
+    out, ref = _run(lens, Q, Hq, 8, 16, causal, seed=21)
+    _check(out, ref)
+
+
+def _packed_specs(K: int, A: int):
+    """Branch specs of Engine._predict (serving/engine.py:98-105): A anchors for
+    each accepted count 1..K-1, then the all-accepted branch."""
+    specs = [(n, 1000 + n * A + a) for n in range(1, K) for a in range(A)]
+    return specs + [(K, None)]
+
+
+@pytest.mark.parametrize("A,Hq,prefixes,ps", [(1, 16, [1024, 517, 33, 2048], 16), (3, 16, [200, 95], 16),
+                                              (1, 32, [640, 1], 16), (1, 16, [300, 700], 256)])
+def test_packed_block_matches_engine_mask(A, Hq, prefixes, ps):
+    """Packed draft attention against the fp64 oracle under Engine._mask."""
+    K = 16
+    specs = _packed_specs(K, A)
+    Q = K * (1 + len(specs))
+    lens = [p + Q for p in prefixes]
+    dev = torch.device("cuda:0")
+    kv = workloads.paged_kv(31, lens, Hkv=8, D=128, page_size=ps, device="cpu")
+    q = workloads.queries(37, len(lens), Q, Hq=Hq, D=128)
+    vis = att.packed_visibility(K, [n for n, _ in specs])
+    out = att.packed_block_attn(q.to(dev), kv.k_cache.to(dev), kv.v_cache.to(dev), kv.context_lens.to(dev),
+                                kv.block_table.to(dev), vis.to(dev))
+    torch.cuda.synchronize()
+    masks = [oa.engine_mask(p, Q, p + Q, K, specs) for p in prefixes]
+    ref = oa.paged_attention(q.float().numpy(), kv.k_cache.float().numpy(), kv.v_cache.float().numpy(),
+                             kv.block_table.numpy(), kv.context_lens.numpy(), 1.0 / math.sqrt(128), masks=masks)
+    _check(out, ref)
+
+
+def test_packed_recovery_descriptor_equals_bidirectional_block():
+    """A visibility of {Q, 0, 0} on every row is the recovery mask (d3d_draft_block_attn)."""
+    dev = torch.device("cuda:0")
+    lens = [1024 + 16, 77 + 16]
+    kv = workloads.paged_kv(5, lens, Hkv=8, D=128, page_size=16, device="cpu")
+    q = workloads.queries(6, 2, 16, Hq=16, D=128).to(dev)
+    args = (kv.k_cache.to(dev), kv.v_cache.to(dev), kv.context_lens.to(dev), kv.block_table.to(dev))
+    vis = torch.tensor([[16, 0, 0]] * 16, dtype=torch.int32, device=dev)
+    a = att.packed_block_attn(q, *args, vis)
+    b = att.draft_block_attn(q, *args)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

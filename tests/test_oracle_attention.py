@@ -91,3 +91,21 @@ def test_fp32_torch_restatement_matches_fp64_oracle():
         b = oa.paged_attention(q.float().numpy(), kv.k_cache.float().numpy(), kv.v_cache.float().numpy(),
                                kv.block_table.numpy(), kv.context_lens.numpy(), 128 ** -0.5, causal=causal)
         np.testing.assert_allclose(a.numpy(), b, atol=2e-6)
+
+
+def test_packed_visibility_restates_engine_mask():
+    """d3d_amd.attention.packed_visibility, expanded to a bool mask, equals
+    the oracle's restatement of Engine._mask (serving/engine.py:35-52)."""
+    import numpy as np
+    from d3d_amd.attention import packed_visibility
+    from oracle.attention import engine_mask
+    K = 16
+    for A in (1, 2, 3):
+        specs = [(n, 7) for n in range(1, K) for _ in range(A)] + [(K, None)]
+        Q = K * (1 + len(specs))
+        vis = packed_visibility(K, [n for n, _ in specs]).numpy()
+        for prefix in (0, 5, 1024):
+            S = prefix + Q
+            t = np.arange(S)[None, :]
+            got = (t < prefix + vis[:, :1]) | ((t >= prefix + vis[:, 1:2]) & (t < prefix + vis[:, 2:3]))
+            np.testing.assert_array_equal(got, engine_mask(prefix, Q, S, K, specs))
