@@ -56,6 +56,54 @@ __global__ __launch_bounds__(NT) void conf_stats_kernel(Params P) {
     if (threadIdx.x == 0) P.stats[((size_t)b * P.Q + i) * P.C + c] = st;
 }
 
+// Among positions with mask[i], the k highest confidences (ties: lower
+// position; all of them when k >= their count) take x0 in block; selected
+// (may be null) records which positions were unmasked.  Rank of position i:
+// the number of masked positions with higher confidence, or equal
+// confidence and a lower index.
+__device__ __forceinline__ void rank_and_unmask(int64_t* block, int Q, int k, int n_masked, const uint8_t* mask,
+                                                const float* conf, const int* x0, uint8_t* selected) {
+    const int kk = min(k, n_masked);
+    for (int i = threadIdx.x; i < Q; i += NT) {
+        bool pick = false;
+        if (mask[i]) {
+            const float ci = conf[i];
+            int rank = 0;
+            for (int j = 0; j < Q; ++j)
+                if (mask[j] && (conf[j] > ci || (conf[j] == ci && j < i))) ++rank;
+            pick = rank < kk;
+            if (pick) block[i] = x0[i];
+        }
+        if (selected) selected[i] = pick;
+    }
+}
+
+// Top-k unmask with caller-given tokens and confidences (the sampled draft
+// path): one workgroup per request.
+__global__ __launch_bounds__(NT) void select_transfer_kernel(int64_t* block, int64_t mask_id, int k,
+                                                             const int64_t* x0, const float* conf,
+                                                             uint8_t* selected, int Q) {
+    const int b = blockIdx.x;
+    __shared__ float sC[kMaxQ];
+    __shared__ int sX[kMaxQ];
+    __shared__ uint8_t sMask[kMaxQ];
+    __shared__ int s_masked;
+    if (threadIdx.x == 0) s_masked = 0;
+    __syncthreads();
+    int local = 0;
+    for (int i = threadIdx.x; i < Q; i += NT) {
+        const size_t e = (size_t)b * Q + i;
+        sMask[i] = block[e] == mask_id;
+        sC[i] = conf[e];
+        sX[i] = (int)x0[e];
+        local += sMask[i];
+    }
+    if (local) atomicAdd(&s_masked, local);  // LDS atomic
+    __syncthreads();
+    rank_and_unmask(block + (size_t)b * Q, Q, k, s_masked, sMask, sC, sX,
+                    selected ? selected + (size_t)b * Q : nullptr);
+}
+
 __global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
     const int b = blockIdx.x;
     const int Q = P.Q;
@@ -83,17 +131,7 @@ __global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
         s_masked = n;
     }
     __syncthreads();
-    const int kk = min(P.k, s_masked);
-    // Rank of a masked position among masked positions: higher confidence
-    // first, then lower index.
-    for (int i = threadIdx.x; i < Q; i += NT) {
-        if (!sMask[i]) continue;
-        const float ci = sS[i];
-        int rank = 0;
-        for (int j = 0; j < Q; ++j)
-            if (sMask[j] && (sS[j] > ci || (sS[j] == ci && j < i))) ++rank;
-        if (rank < kk) P.block[(size_t)b * Q + i] = sArg[i];
-    }
+    rank_and_unmask(P.block + (size_t)b * Q, Q, P.k, s_masked, sMask, sS, sArg, nullptr);
 }
 
 template <int DT, bool VEC>
@@ -113,6 +151,17 @@ using namespace d3d;
 extern "C" size_t d3d_confidence_workspace_bytes(int B, int Q, int64_t V) {
     if (B < 1 || Q < 1 || V < 1) return 0;
     return ((size_t)B * Q * conf::num_chunks(V) * sizeof(rows::RowStat) + 255) & ~(size_t)255;
+}
+
+extern "C" int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, const int64_t* x0,
+                                   const float* conf, uint8_t* selected_out, int B, int Q, void* stream) {
+    using namespace conf;
+    if (B < 1 || B > 65535 || Q < 1 || Q > kMaxQ || k < 0) return D3D_E_SHAPE;
+    if (!block_ids || !x0 || !conf) return D3D_E_NULL;
+    hipLaunchKernelGGL(select_transfer_kernel, dim3(B), dim3(rows::NT), 0, static_cast<hipStream_t>(stream),
+                       block_ids, mask_id, k, x0, conf, selected_out, Q);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
 }
 
 extern "C" int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids, int64_t mask_id,

@@ -26,7 +26,7 @@ namespace topk {
 
 using namespace rows;
 
-constexpr int kMaxK = 16;
+constexpr int kMaxK = 64;
 constexpr int kMaxCand = 8192;  // chunk candidates per row merged in LDS
 
 struct Cand {

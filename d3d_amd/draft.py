@@ -2,6 +2,13 @@
 
 Mirrors single/eval_sync.py:
 
+* ``sample_tokens`` / ``sample_with_prob`` -- :308-338, proposal draws
+                                  (argmax at T <= 1e-5, else the inverse
+                                  CDF of softmax(logits / T) at a uniform)
+* ``sample_with_sparse_probs`` -- :341-367, top-S support and a draw from it
+* ``select_transfer``          -- :447-465 with caller-given tokens and
+                                  confidences (the sampled path)
+
 * ``get_num_transfer_tokens``  -- :440-444, the per-step unmask schedule
 * ``confidence_topk_unmask``   -- :447-465 (_select_transfer, low-confidence
                                   remasking) with the greedy confidence of
@@ -60,6 +67,91 @@ def confidence_topk_unmask(logits: torch.Tensor, block: torch.Tensor, mask_id: i
     return x0, conf
 
 
+def _uniforms(shape, dev, uniforms, generator):
+    if uniforms is None:
+        uniforms = torch.rand(shape, device=dev, generator=generator)
+    return uniforms.to(device=dev, dtype=torch.float32).reshape(shape).contiguous()
+
+
+def sample_with_prob(logits: torch.Tensor, temperature: float = 0.0, *, uniforms: Optional[torch.Tensor] = None,
+                     generator: Optional[torch.Generator] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(tokens [...], probs [...]) of logits [..., V]: single/eval_sync.py:324-338.
+
+    T <= 1e-5: the argmax with probability 1.  Otherwise the token is the
+    inverse-CDF draw of softmax(logits / T) at ``uniforms`` (one per row,
+    drawn with torch.rand when omitted) and probs its probability.
+    """
+    dev = _lib.require_device(logits)
+    lg = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
+    lg = lg.contiguous()
+    V = lg.shape[-1]
+    N = lg.numel() // V
+    greedy = not temperature > 1e-5
+    u = None if greedy else _uniforms(lg.shape[:-1], dev, uniforms, generator)
+    tok = torch.empty(lg.shape[:-1], dtype=torch.int64, device=dev)
+    prob = torch.empty(lg.shape[:-1], dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws = _lib.workspace(dev, "sample", lib.d3d_sample_workspace_bytes(max(N, 1), V))
+    st = lib.d3d_sample_rows(lg.data_ptr(), _lib.dtype_code(lg), N, V, float(temperature), _lib.ptr(u),
+                             tok.data_ptr(), prob.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_sample_rows")
+    return tok, prob
+
+
+def sample_tokens(logits: torch.Tensor, temperature: float = 0.0, *, uniforms: Optional[torch.Tensor] = None,
+                  generator: Optional[torch.Generator] = None) -> torch.Tensor:
+    """single/eval_sync.py:308-321: the tokens of :func:`sample_with_prob`."""
+    return sample_with_prob(logits, temperature, uniforms=uniforms, generator=generator)[0]
+
+
+def sample_with_sparse_probs(logits: torch.Tensor, temperature: float, top_k: int, *,
+                             uniforms: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None):
+    """(tokens, support ids [..., S], support probs [..., S]): single/eval_sync.py:341-367.
+
+    T <= 1e-5: the argmax as a support of one with probability 1.  Otherwise
+    the support is the S = top_k largest logits (descending, ties by lower
+    id; 1 <= S <= 64), its probabilities softmax(logits / T) over the
+    support, and the token the inverse-CDF draw from them.
+    """
+    dev = _lib.require_device(logits)
+    if not temperature > 1e-5:
+        tok = topk_tokens(logits, 1)
+        return tok[..., 0], tok, torch.ones(tok.shape, dtype=torch.float32, device=dev)
+    S = int(top_k)
+    if not 1 <= S <= min(64, logits.shape[-1]):
+        raise ValueError("sparse proposals need 1 <= top_k <= 64 support entries")
+    ids, vals = topk_tokens(logits, S, with_values=True)
+    N = ids.numel() // S
+    u = _uniforms(logits.shape[:-1], dev, uniforms, generator)
+    tok = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev)
+    probs = torch.empty(ids.shape, dtype=torch.float32, device=dev)
+    st = _lib.load().d3d_sample_support(vals.data_ptr(), ids.data_ptr(), N, S, float(temperature), u.data_ptr(),
+                                        tok.data_ptr(), probs.data_ptr(), None, _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_sample_support")
+    return tok, ids, probs
+
+
+def select_transfer(block: torch.Tensor, mask_id: int, k: int, x0: torch.Tensor,
+                    conf: torch.Tensor) -> torch.Tensor:
+    """Unmask the k most confident masked positions of each request in place.
+
+    single/eval_sync.py:447-465 with caller-given x0 [B, Q] and confidences
+    [B, Q] (ties: lowest position); returns the unmasked positions [B, Q]
+    bool.  Selection is per request.
+    """
+    dev = _lib.require_device(block, x0, conf)
+    if block.ndim != 2 or block.dtype != torch.int64 or not block.is_contiguous():
+        raise ValueError("block must be a contiguous int64 [B, Q] tensor (updated in place)")
+    B, Q = block.shape
+    x0 = x0.to(torch.int64).reshape(B, Q).contiguous()
+    conf = conf.to(torch.float32).reshape(B, Q).contiguous()
+    sel = torch.empty(B, Q, dtype=torch.uint8, device=dev)
+    st = _lib.load().d3d_select_transfer(block.data_ptr(), int(mask_id), int(k), x0.data_ptr(), conf.data_ptr(),
+                                         sel.data_ptr(), B, Q, _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_select_transfer")
+    return sel.bool()
+
+
 def topk_tokens(logits: torch.Tensor, k: int, with_values: bool = False):
     """Top-k token ids [..., k] int64 of logits [..., V] (fp32 or bf16), one launch pair.
 
@@ -96,24 +188,42 @@ def draft_block_forward(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequen
 
 
 def d3d_draft_block(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], block: torch.Tensor,
-                    denoising_steps: int, *, mask_id: int = MASK_ID, temperature: float = 0.0,
-                    name: str = "draft", graphs: Optional[dict] = None, width: Optional[int] = None) -> torch.Tensor:
+                    denoising_steps: int, *, mask_id: int = MASK_ID, temperature: float = 0.0, top_k: int = 0,
+                    name: str = "draft", graphs: Optional[dict] = None, width: Optional[int] = None,
+                    uniforms: Optional[torch.Tensor] = None, generator: Optional[torch.Generator] = None,
+                    return_proposal: Optional[str] = None):
     """Denoise a block [B, Q] whose masked positions hold ``mask_id``.
 
-    single/eval_sync.py:482-592 with greedy low-confidence remasking: each
-    step runs the draft over the block, then unmasks the scheduled number of
-    most confident masked positions; the last step fills every remaining
-    mask.  ``num_masks`` is taken from request 0, as the reference's
-    schedule is (:503-508).
+    single/eval_sync.py:482-592 with low-confidence remasking: each step
+    runs the draft over the block, then unmasks the scheduled number of most
+    confident masked positions; the last step fills every remaining mask.
+    ``num_masks`` is taken from request 0, as the reference's schedule is
+    (:503-508).
 
-    With a ``graphs`` dict each (forward + unmask) step is replayed from a
-    HIP graph cached there per (B, Q, k, table width); ``width`` fixes the
-    page-table width (default: the current longest table).
+    T <= 1e-5: x0 is the argmax and the confidence its softmax probability
+    (one fused kernel per step).  T > 1e-5: x0 is drawn from softmax(logits
+    / T) (dense) or from the top-``top_k`` support (``return_proposal=
+    "sparse"``) at ``uniforms`` [steps, B, Q] (torch.rand when omitted), and
+    the confidence is the drawn token's probability (:560-576).
+
+    ``return_proposal`` (T > 1e-5): ``"logits"`` also returns the draft
+    logits row of every position at the step it was unmasked -- the proposal
+    q = softmax(row / T) that the reference keeps as proposal_probs
+    (:577-584), consumed by the acceptance kernel directly -- and
+    ``"sparse"`` returns (support ids [B, Q, S], support probs [B, Q, S])
+    (:585-589).
+
+    With a ``graphs`` dict (greedy mode) each (forward + unmask) step is
+    replayed from a HIP graph cached there per (B, Q, k, table width);
+    ``width`` fixes the page-table width (default: the current longest table).
     """
     cur = block.clone().contiguous()
     num_masks = int((cur[0] == mask_id).sum().item())
+    stochastic = temperature > 1e-5
+    if return_proposal not in (None, "logits", "sparse"):
+        raise ValueError("return_proposal must be None, 'logits' or 'sparse'")
     if num_masks == 0:
-        return cur
+        return (cur, None) if return_proposal else cur
     schedule = get_num_transfer_tokens(num_masks, denoising_steps)
     B, Q = cur.shape
     starts = [s.prefix for s in seqs]
@@ -121,19 +231,41 @@ def d3d_draft_block(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence],
         reserve(kv, s, name, s.prefix + Q)
     tables, slots, lens, logical, _ = block_inputs(kv, seqs, name, starts, Q, drafter.device, width)
     W = tables.shape[1]
+    if stochastic:
+        u_all = uniforms if uniforms is not None else torch.rand(len(schedule), B, Q, device=cur.device,
+                                                                 generator=generator)
+        u_all = u_all.to(device=cur.device, dtype=torch.float32).reshape(len(schedule), B, Q)
+    proposal = None
     for step, k in enumerate(schedule):
         if step == len(schedule) - 1:
             k = Q  # the last step unmasks everything left (:549-550)
-        if graphs is None:
-            hidden = drafter(cur, logical, kv, tables, lens, slots, causal=False, max_context=W * kv.page_size)
-            confidence_topk_unmask(drafter.logits(hidden), cur, mask_id, k, temperature)
+        if not stochastic and graphs is not None:
+            key = (B, Q, k, W, temperature)
+            step_fn = graphs.get(key)
+            if step_fn is None:
+                def post(hidden, ids, k=k):
+                    confidence_topk_unmask(drafter.logits(hidden), ids, mask_id, k, temperature)
+                    return ids
+                step_fn = graphs[key] = BlockStep(drafter, kv, B, Q, W, causal=False, post=post)
+            cur.copy_(step_fn(cur, logical, tables, slots, lens))
             continue
-        key = (B, Q, k, W, temperature)
-        step_fn = graphs.get(key)
-        if step_fn is None:
-            def post(hidden, ids, k=k):
-                confidence_topk_unmask(drafter.logits(hidden), ids, mask_id, k, temperature)
-                return ids
-            step_fn = graphs[key] = BlockStep(drafter, kv, B, Q, W, causal=False, post=post)
-        cur.copy_(step_fn(cur, logical, tables, slots, lens))
+        hidden = drafter(cur, logical, kv, tables, lens, slots, causal=False, max_context=W * kv.page_size)
+        logits = drafter.logits(hidden)
+        if not stochastic:
+            confidence_topk_unmask(logits, cur, mask_id, k, temperature)
+            continue
+        if return_proposal == "sparse":
+            x0, ids, probs = sample_with_sparse_probs(logits, temperature, top_k, uniforms=u_all[step])
+            conf = probs.gather(-1, (ids == x0[..., None]).long().argmax(-1, keepdim=True))[..., 0]
+        else:
+            x0, conf = sample_with_prob(logits, temperature, uniforms=u_all[step])
+        sel = select_transfer(cur, mask_id, k, x0, conf)
+        if return_proposal == "logits":
+            proposal = logits.clone() if proposal is None else torch.where(sel[..., None], logits, proposal)
+        elif return_proposal == "sparse":
+            if proposal is None:
+                proposal = (torch.zeros_like(ids), torch.zeros_like(probs))
+            proposal = (torch.where(sel[..., None], ids, proposal[0]), torch.where(sel[..., None], probs, proposal[1]))
+    if return_proposal:
+        return cur, proposal
     return cur

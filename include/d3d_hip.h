@@ -222,6 +222,20 @@ int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids
                                float* conf_out, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/*
+ * Top-k unmask with caller-given tokens and confidences: among positions
+ * with block_ids == mask_id, the k highest conf (ties: lowest position; all
+ * of them when k >= their count) take x0, in place; selected_out [B, Q]
+ * uint8 (may be NULL) marks the positions unmasked.  x0 [B, Q] int64, conf
+ * [B, Q] fp32, Q <= 1024.
+ *
+ * Replaces _select_transfer, single/eval_sync.py:447-465, when x0 and its
+ * confidence come from the sampled proposal (_sample_with_prob or the
+ * sparse support, single/eval_sync.py:560-576); selection is per request.
+ */
+int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, const int64_t* x0,
+                        const float* conf, uint8_t* selected_out, int B, int Q, void* stream);
+
 /* Bytes of workspace d3d_topk_rows needs. */
 size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
 
@@ -229,7 +243,7 @@ size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
  * Top-k token ids of N logits rows [N, V] (fp32 or bf16): ids_out [N, k]
  * int64 in descending order of value, equal values by ascending id (so
  * ids_out[n][0] is the argmax with torch's first-maximum rule); NaN entries
- * are never selected.  vals_out [N, k] fp32 may be NULL.  1 <= k <= 16,
+ * are never selected.  vals_out [N, k] fp32 may be NULL.  1 <= k <= 64,
  * N <= 65535, ceil(V / 4096) * k <= 8192.
  *
  * Replaces logits.argmax(-1) and logits.topk(k).indices in Runner._run,
@@ -238,6 +252,39 @@ size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
  */
 int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int64_t* ids_out,
                   float* vals_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace d3d_sample_rows needs. */
+size_t d3d_sample_workspace_bytes(int N, int64_t V);
+
+/*
+ * One proposal token per logits row [N, V] (fp32 or bf16) and its
+ * probability.  temperature <= 1e-5: the argmax (first maximum) with
+ * probability 1 (uniforms unused, may be NULL).  Otherwise p =
+ * softmax(logits / T) and token = the first t with C_t > u[n] * W over the
+ * softmax weights, else the last t with positive weight (inverse CDF in
+ * place of torch.multinomial); probs_out[n] = p[token] (may be NULL).
+ * N <= 65535.  D3D_TOKEN_EMPTY_DISTRIBUTION if a row has no finite entry.
+ *
+ * Replaces _sample_tokens / _sample_with_prob over _sampling_probs,
+ * single/eval_sync.py:287-338 (top-k / top-p filtering off).
+ */
+int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
+                    const float* uniforms, int64_t* tokens_out, float* probs_out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse proposal over a top-S support: support_vals / support_ids [N, S]
+ * are the S largest logits of each row in descending order with their ids
+ * (d3d_topk_rows).  support_probs_out [N, S] = softmax(support_vals / T);
+ * tokens_out[n] = support_ids[n, s] for the first s whose inclusive sum
+ * exceeds u[n] * W (else the last positive entry); token_probs_out (may be
+ * NULL) the drawn entry's probability.  1 <= S <= 64, temperature > 1e-5.
+ *
+ * Replaces _sample_with_sparse_probs, single/eval_sync.py:341-367.
+ */
+int d3d_sample_support(const float* support_vals, const int64_t* support_ids, int N, int S,
+                       float temperature, const float* uniforms, int64_t* tokens_out,
+                       float* support_probs_out, float* token_probs_out, void* stream);
 
 /*
  * Residual add + RMSNorm over rows of H bf16 entries (H a multiple of 8,

@@ -165,3 +165,48 @@ def num_transfer_tokens(num_masks: int, steps: int):
     steps = max(1, int(steps))
     base, extra = divmod(int(num_masks), steps)
     return [base + (1 if i < extra else 0) for i in range(steps)]
+
+
+def sample_with_prob(logits, temperature: float, uniforms):
+    """single/eval_sync.py:324-338 (_sample_with_prob over _sampling_probs),
+    with torch.multinomial replaced by the inverse CDF of each row's fp64
+    softmax at u[n].  Returns (tokens, probs, margins) per row of [N, V];
+    T <= 1e-5 gives the argmax with probability 1 (margin inf)."""
+    x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
+    u = np.asarray(uniforms, np.float64).reshape(-1)
+    N = x.shape[0]
+    tok = np.zeros(N, np.int64)
+    prob = np.zeros(N, np.float64)
+    margin = np.full(N, np.inf)
+    for n in range(N):
+        p = row_probs(x[n], KIND_LOGITS, temperature)
+        if temperature <= 1e-5:
+            tok[n] = int(np.argmax(p))
+        else:
+            tok[n], margin[n] = inverse_cdf(p, u[n])
+        prob[n] = p[tok[n]]
+    return tok, prob, margin
+
+
+def sample_sparse(logits, temperature: float, S: int, uniforms):
+    """single/eval_sync.py:341-367 (_sample_with_sparse_probs), fp64: the S
+    largest entries of logits / T (descending, ties by lower id), softmax over
+    them, inverse-CDF draw at u[n].  Returns (tokens, ids [N,S], probs [N,S],
+    margins)."""
+    x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
+    u = np.asarray(uniforms, np.float64).reshape(-1)
+    N, V = x.shape
+    ids = np.zeros((N, S), np.int64)
+    probs = np.zeros((N, S), np.float64)
+    tok = np.zeros(N, np.int64)
+    margin = np.zeros(N)
+    for n in range(N):
+        z = x[n].astype(np.float64) / temperature
+        order = np.lexsort((np.arange(V), -z))[:S]
+        zs = z[order]
+        e = np.exp(zs - zs.max())
+        ids[n] = order
+        probs[n] = e / e.sum()
+        local, margin[n] = inverse_cdf(probs[n], u[n])
+        tok[n] = order[local]
+    return tok, ids, probs, margin
