@@ -8,7 +8,9 @@
 //       the anchor tokens of the packed branches
 //
 // Order: descending value, equal values by ascending index, so top[0] is
-// torch.argmax's first maximum.  NaN entries are never selected.
+// torch.argmax's first maximum.  NaN entries are never selected.  With
+// log_softmax the values are returned as log-probabilities x - logsumexp(x)
+// (single/eval_sync.py:763-768, torch.topk of log_softmax: the same ids).
 //
 // Two kernels: (1) grid (chunks, rows): each workgroup takes k rounds of a
 // workgroup argmax over its 4096-entry chunk (each thread holds 16 entries
@@ -38,6 +40,7 @@ struct Params {
     const void* logits;  // [N, V]
     int N, V, C, k;
     Cand* cand;       // [N][C][k]
+    float2* lse;      // [N][C] chunk (max, sum exp(x - max)) when log-probabilities are asked for
     int64_t* ids;     // [N, k]
     float* vals;      // [N, k] (may be null)
 };
@@ -69,6 +72,17 @@ __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
         for (int l = 0; l < L; ++l)
             if (tile_index<DT>(first, NT * E, l) == wi) taken |= 1u << l;
         if (threadIdx.x == 0) P.cand[((size_t)n * P.C + c) * P.k + r] = Cand{wv, wi};
+        if (r == 0 && P.lse) {
+            // Round 0's winner is the chunk max: the chunk's share of logsumexp.
+            float se = 0.f;
+            if (wv != -INFINITY) {
+#pragma unroll
+                for (int l = 0; l < L; ++l)
+                    if (tile_index<DT>(first, NT * E, l) < P.V) se += expf(x[l] - wv);
+            }
+            se = block_sum<NT>(se, sv);
+            if (threadIdx.x == 0) P.lse[(size_t)n * P.C + c] = make_float2(wv, se);
+        }
     }
 }
 
@@ -79,6 +93,20 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(Params P) {
     __shared__ int si[NT / kWave];
     const int total = P.C * P.k;
     for (int e = threadIdx.x; e < total; e += NT) lds[e] = P.cand[(size_t)n * total + e];
+    float logz = 0.f;
+    if (P.lse) {
+        // logsumexp over the chunk records, in a fixed order.
+        float mx = -INFINITY;
+        for (int c = threadIdx.x; c < P.C; c += NT) mx = fmaxf(mx, P.lse[(size_t)n * P.C + c].x);
+        mx = block_max<NT>(mx, sv);
+        float se = 0.f;
+        for (int c = threadIdx.x; c < P.C; c += NT) {
+            const float2 t = P.lse[(size_t)n * P.C + c];
+            if (t.x != -INFINITY) se += t.y * expf(t.x - mx);
+        }
+        se = block_sum<NT>(se, sv);
+        logz = mx + logf(se);
+    }
     __syncthreads();
     for (int r = 0; r < P.k; ++r) {
         float bv = -INFINITY;
@@ -96,7 +124,7 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(Params P) {
         block_argmax<NT>(wv, wi, sv, si);
         if (threadIdx.x == 0) {
             P.ids[(size_t)n * P.k + r] = wi == INT_MAX ? -1 : wi;
-            if (P.vals) P.vals[(size_t)n * P.k + r] = wv;
+            if (P.vals) P.vals[(size_t)n * P.k + r] = P.lse ? wv - logz : wv;
         }
         // Token ids are unique among candidates: the holder marks its entry.
         if (bp >= 0 && bi == wi && wi != INT_MAX) lds[bp].i = INT_MAX;
@@ -109,15 +137,20 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(Params P) {
 
 using namespace d3d;
 
+static size_t cand_bytes(int N, int64_t V, int k) {
+    const size_t C = (size_t)((V + rows::kChunk - 1) / rows::kChunk);
+    return ((size_t)N * C * k * sizeof(topk::Cand) + 255) & ~(size_t)255;
+}
+
 extern "C" size_t d3d_topk_workspace_bytes(int N, int64_t V, int k) {
     if (N < 1 || V < 1 || k < 1) return 0;
     const size_t C = (size_t)((V + rows::kChunk - 1) / rows::kChunk);
-    const size_t b = (size_t)N * C * k * sizeof(topk::Cand);
-    return (b + 255) & ~(size_t)255;
+    return cand_bytes(N, V, k) + (((size_t)N * C * sizeof(float2) + 255) & ~(size_t)255);
 }
 
-extern "C" int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int64_t* ids_out,
-                             float* vals_out, void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int log_softmax,
+                             int64_t* ids_out, float* vals_out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
     using namespace topk;
     if (N < 0 || V < 1 || V > INT_MAX / 2 || k < 1 || k > kMaxK || k > V) return D3D_E_SHAPE;
     if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
@@ -133,6 +166,9 @@ extern "C" int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, in
     if ((int64_t)P.C * k > kMaxCand) return D3D_E_SHAPE;
     if (workspace_bytes < d3d_topk_workspace_bytes(N, V, k)) return D3D_E_WORKSPACE;
     P.cand = static_cast<Cand*>(workspace);
+    P.lse = (log_softmax && vals_out)
+                ? reinterpret_cast<float2*>(static_cast<char*>(workspace) + cand_bytes(N, V, k))
+                : nullptr;
     P.ids = ids_out;
     P.vals = vals_out;
     const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;

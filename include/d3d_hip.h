@@ -243,15 +243,19 @@ size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
  * Top-k token ids of N logits rows [N, V] (fp32 or bf16): ids_out [N, k]
  * int64 in descending order of value, equal values by ascending id (so
  * ids_out[n][0] is the argmax with torch's first-maximum rule); NaN entries
- * are never selected.  vals_out [N, k] fp32 may be NULL.  1 <= k <= 64,
- * N <= 65535, ceil(V / 4096) * k <= 8192.
+ * are never selected.  vals_out [N, k] fp32 may be NULL; with log_softmax
+ * != 0 it holds log_softmax(x) of the selected entries (x - logsumexp(x)),
+ * else the raw values.  1 <= k <= 64, N <= 65535, ceil(V / 4096) * k <= 8192.
  *
  * Replaces logits.argmax(-1) and logits.topk(k).indices in Runner._run,
  * serving/backend.py:84-93, which feed the anchor choice of
- * Engine._recover / Engine._predict (serving/engine.py:54-131).
+ * Engine._recover / Engine._predict (serving/engine.py:54-131), and
+ * torch.topk(log_softmax(logits), k) of the anchor draft,
+ * single/eval_sync.py:763-768.
  */
-int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int64_t* ids_out,
-                  float* vals_out, void* workspace, size_t workspace_bytes, void* stream);
+int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int log_softmax,
+                  int64_t* ids_out, float* vals_out, void* workspace, size_t workspace_bytes,
+                  void* stream);
 
 /* Bytes of workspace d3d_sample_rows needs. */
 size_t d3d_sample_workspace_bytes(int N, int64_t V);

@@ -132,3 +132,60 @@ def test_denoise_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(got, eager)
         assert torch.equal(dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id), eager)
+
+
+@pytest.mark.parametrize("mode", ["block_causal", "causal"])
+def test_fused_commit_matches_restatement(mode):
+    """single/eval_sync.py:596-775: pending tokens committed to the draft cache
+    in the same forward as the anchor block (mask of :251-275), top-2
+    log-probabilities of the last step, then a later block that reads the
+    committed K/V."""
+    dev = torch.device("cuda:0")
+    model = Qwen3PagedModel(TINY, dev, draft=True, seed=13, init_std=0.05)
+    model.lm_head.mul_(20.0)
+    kv = PagedKV(TINY, 64, 16, dev)
+    g = torch.Generator().manual_seed(6)
+    mask_id = TINY.vocab - 1
+    prompts = torch.randint(0, mask_id, (2, 32), generator=g)
+    pending = torch.randint(0, mask_id, (2, 5), generator=g)
+    seqs = [Sequence(i, p.tolist()) for i, p in enumerate(prompts)]
+    prefill(model, kv, seqs, "draft")
+    for s in seqs:
+        s.prefix += 5  # committed, K/V not written yet
+    block = torch.full((2, 16), mask_id, dtype=torch.int64)
+    block[:, 0] = torch.tensor([3, 4])
+    cur, metrics = dr.d3d_draft_block_fused_commit(model, kv, seqs, block.to(dev), pending.to(dev), 1,
+                                                   mask_id=mask_id, attention_mask_mode=mode, return_topk=2)
+    W = model_ref.weights_fp32(model)
+    T = 32 + 5 + 16
+    for b in range(2):
+        ids = torch.cat([prompts[b], pending[b], block[b]])
+        mask = torch.ones(T, T).tril().bool()
+        if mode == "block_causal":
+            mask[32:37, :37] = True  # pending rows see every pending token
+        mask[37:, :] = True  # block rows see everything
+        ref = model_ref.forward(W, TINY, ids, torch.arange(T), mask)[37:]
+        lp = torch.log_softmax(ref, -1)
+        top2 = ref.topk(3, -1)
+        sure = (top2.values[:, 1] - top2.values[:, 2]) > 0.05 * ref.std(-1)
+        sure &= (top2.values[:, 0] - top2.values[:, 1]) > 0.05 * ref.std(-1)
+        assert sure.float().mean() >= 0.25  # both top-2 gaps decisive
+        got_ids = metrics["top_tokens"][b].cpu()
+        assert torch.equal(got_ids[sure], top2.indices[sure, :2])
+        got_lp = metrics["top_logprobs"][b].cpu()
+        ref_lp = lp.gather(-1, got_ids)
+        assert float((got_lp - ref_lp).abs().max()) <= 5e-2 * float(ref.abs().max())
+        # one step: every mask takes the greedy token, the anchor stays
+        assert cur[b, 0].item() == block[b, 0].item()
+        assert torch.equal(cur[b, 1:].cpu()[sure[1:]], ref.argmax(-1)[1:][sure[1:]])
+    # A later block reads the committed pending K/V.
+    nxt = torch.randint(0, mask_id, (2, 16), generator=g)
+    got = dr.draft_block_forward(model, kv, seqs, nxt.to(dev), "draft")
+    for b in range(2):
+        ids = torch.cat([prompts[b], pending[b], nxt[b]])
+        mask = torch.ones(T, T).tril().bool()
+        if mode == "block_causal":
+            mask[32:37, :37] = True
+        mask[37:, :] = True
+        ref = model_ref.forward(W, TINY, ids, torch.arange(T), mask)[37:]
+        _close(got[b], ref)
