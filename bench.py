@@ -42,6 +42,9 @@ def _parse():
     ap.add_argument("--no-models", action="store_true",
                     help="skip the draft-block (1.7B) and end-to-end (8B + 1.7B) model runs")
     ap.add_argument("--e2e-new-tokens", type=int, default=512)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain 64 MiB device copy 5 times (the reference kernel for "
+                         "scaling FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -219,6 +222,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     from d3d_amd import workloads
+
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
 
     # Headline step: block-verify attention (batch 1, Qwen3-8B GQA 32/8, d 128, K=16
     # causal block over a 2048-token prefix in 16-token pages of a shuffled

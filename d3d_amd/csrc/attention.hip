@@ -22,7 +22,12 @@
 // [B, max_pages] int32; context_lens [B] int32 = prefix + Q (the block's own
 // keys are already appended).
 //
-// Work decomposition: workgroup (split, kv_head, b * query tiles + tile).
+// Work decomposition: workgroup (work item * Hkv + kv_head, query tile).
+// Request b's context is cut into S_b = ceil(ctx_b / split_tokens) splits
+// of whole 64-token tiles; for up to kMaxPackedB requests the work items
+// (b, split) are numbered consecutively over the requests' actual split
+// counts, so the grid's tail holds only empty items and short requests leave
+// no idle workgroups in the middle of the launch.
 // The G = Hq/Hkv query heads of the group times QT queries of the block
 // form the MFMA rows (row r = g*QT + qi, 16 rows per wave, at most 128).
 // Key t is visible to a row iff t < A or S_lo <= t < S_hi (two ranges):
@@ -56,6 +61,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
 
 struct Params {
     const uint16_t* q;
@@ -64,18 +70,56 @@ struct Params {
     const int32_t* block_table;
     const int32_t* context_lens;
     uint16_t* out;
-    float* part_o;   // [B][Hkv][splits][M][D]
-    float* part_ml;  // [B][Hkv][splits][M][2]
+    _Float16* part_o;  // [B][nqt][Hkv][splits][M][D], O / l per split
+    float* part_ml;    // [B][nqt][Hkv][splits][M][2], (m, l) per split
     int B, Q, Hq, Hkv, G, M;
     int page_size, max_pages, num_pages;
     int page_shift;  // log2(page_size) for powers of two, else -1
-    int split_tokens, num_splits;
+    int split_tokens, num_splits;  // tokens per split, splits per request at most
     int QT, nqt;        // queries per workgroup, query tiles per request
     const int32_t* vis; // packed mode: [Q][3] visibility descriptor
     float scale_log2;   // softmax scale * log2(e)
 };
 
 enum : int { kCausal = 0, kFull = 1, kPacked = 2 };
+
+constexpr int kMaxPackedB = 64;  // requests whose work items are numbered consecutively
+
+// Splits of request b: at least 1, at most num_splits (keys past
+// num_splits * split_tokens, beyond the max_context bound, are not read).
+__device__ __forceinline__ int splits_of(const Params& P, int b) {
+    const int ctx = min(P.context_lens[b], P.max_pages * P.page_size);
+    const int n = ctx > 0 ? (ctx + P.split_tokens - 1) / P.split_tokens : 1;
+    return min(n, P.num_splits);
+}
+
+// Work item -> (request, split); b = -1 past the last item.
+__device__ __forceinline__ void item_of(const Params& P, int item, int& b, int& s, int& nsplit) {
+    b = -1;
+    s = 0;
+    nsplit = 1;
+    if (P.B <= kMaxPackedB) {
+        int acc = 0;
+        for (int i = 0; i < P.B; ++i) {
+            const int si = splits_of(P, i);
+            if (item < acc + si) {
+                b = i;
+                s = item - acc;
+                nsplit = si;
+                return;
+            }
+            acc += si;
+        }
+    } else {
+        const int bi = item / P.num_splits, si = item - bi * P.num_splits;
+        const int n = splits_of(P, bi);
+        if (si < n) {
+            b = bi;
+            s = si;
+            nsplit = n;
+        }
+    }
+}
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -142,8 +186,10 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
 template <int NW, int MODE>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
     constexpr int NT = NW * 64;
-    const int s = blockIdx.x, kvh = blockIdx.y;
-    const int b = blockIdx.z / P.nqt, qt = blockIdx.z - b * P.nqt;
+    const int kvh = blockIdx.x % P.Hkv, qt = blockIdx.y;
+    int b, s, nsplit;
+    item_of(P, blockIdx.x / P.Hkv, b, s, nsplit);
+    if (b < 0) return;  // past the last work item (uniform, before any barrier)
     const int q0 = qt * P.QT;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g4 = lane >> 4, c16 = lane & 15;
@@ -376,8 +422,8 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
 
-    if (P.num_splits == 1) {
-        const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    if (nsplit == 1) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int orow = w * 16 + 4 * g4 + r;
@@ -394,17 +440,20 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             }
         }
     } else {
-        const size_t unit = ((size_t)blockIdx.z * P.Hkv + kvh) * P.num_splits + s;
-        float* po = P.part_o + unit * P.M * D;
+        // Normalised partial O / l in fp16 (|O / l| <= max |v|), (m, l) in fp32.
+        const size_t unit = (((size_t)b * P.nqt + qt) * P.Hkv + kvh) * P.num_splits + s;
+        _Float16* po = P.part_o + unit * P.M * D;
         float* pml = P.part_ml + unit * P.M * 2;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int orow = w * 16 + 4 * g4 + r;
+            const float sc_r = __shfl(inv, 4 * g4 + r, 64);
             if (orow < P.M) {
 #pragma unroll
                 for (int h = 0; h < D / 64; ++h) {
-                    const f32x4 v = {o[4 * h + 0][r], o[4 * h + 1][r], o[4 * h + 2][r], o[4 * h + 3][r]};
-                    *reinterpret_cast<f32x4*>(po + (size_t)orow * D + 64 * h + 4 * c16) = v;
+                    const h16x4 v = {(_Float16)(o[4 * h + 0][r] * sc_r), (_Float16)(o[4 * h + 1][r] * sc_r),
+                                     (_Float16)(o[4 * h + 2][r] * sc_r), (_Float16)(o[4 * h + 3][r] * sc_r)};
+                    *reinterpret_cast<h16x4*>(po + (size_t)orow * D + 64 * h + 4 * c16) = v;
                 }
             }
         }
@@ -424,8 +473,9 @@ constexpr int kMaxSplits = 256;
 __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y;
     const int b = blockIdx.z / P.nqt, q0 = (blockIdx.z - b * P.nqt) * P.QT;
-    const int S = P.num_splits;
-    const size_t unit0 = ((size_t)blockIdx.z * P.Hkv + kvh) * S;
+    const int S = splits_of(P, b);
+    if (S == 1) return;  // the split kernel wrote this request's output
+    const size_t unit0 = ((size_t)blockIdx.z * P.Hkv + kvh) * P.num_splits;
     __shared__ float wts[kRowsPerCombine][kMaxSplits];
     __shared__ float lsum[kRowsPerCombine][kMaxSplits];
     __shared__ float inv_den[kRowsPerCombine];
@@ -453,7 +503,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
             for (int sp = lane; sp < S; sp += 64) {
                 const float m = wts[rr][sp];
                 const float w = (m == -INFINITY) ? 0.f : exp2f(m - mx);
-                wts[rr][sp] = w;
+                wts[rr][sp] = w * lsum[rr][sp];  // weight of the normalised partial O / l
                 den += w * lsum[rr][sp];
             }
             for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
@@ -468,7 +518,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
 #pragma unroll 8
     for (int sp = 0; sp < S; ++sp) {
         const float w = wts[rr][sp];
-        const f32x4 o = *reinterpret_cast<const f32x4*>(P.part_o + ((unit0 + sp) * P.M + row) * D + c4);
+        const h16x4 h = *reinterpret_cast<const h16x4*>(P.part_o + ((unit0 + sp) * P.M + row) * D + c4);
+        const f32x4 o = {(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
         acc += w * o;
     }
     const float sc = inv_den[rr];
@@ -500,11 +551,9 @@ struct Plan {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Split the context so that a launch has about kTargetWorkgroups workgroups,
-// in whole 64-token tiles.
-// Two workgroups are resident per CU (register-limited) on 256 CUs; twice
-// that many splits absorb requests whose context is shorter than the longest.
-constexpr int kTargetWorkgroups = 1024;
+// Two workgroups are resident per CU (register-limited) on 256 CUs: 512 at
+// a time; about four rounds of work items keep the last round short.
+constexpr int kTargetItems = 2048;
 
 static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
     Plan p;
@@ -514,11 +563,15 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
     const int M = G * p.QT;
     p.waves = M <= 32 ? 2 : (M <= 64 ? 4 : 8);
     const int tiles = (max_context + TILE - 1) / TILE;
-    const int units = B * p.nqt * Hkv;
-    int splits = (kTargetWorkgroups + units - 1) / units;
-    splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
-    splits = splits > kMaxSplits ? kMaxSplits : splits;
-    int tiles_per_split = (tiles + splits - 1) / splits;
+    // Tiles per split: about kTargetItems (request, split, kv head, query
+    // tile) items if every request were max_context long -- several
+    // rounds of the resident workgroups, so that the last round is short,
+    // while each split's fp16 partial stays small against its K/V bytes.
+    const int64_t units = (int64_t)B * p.nqt * Hkv;
+    int64_t tps = (units * tiles + kTargetItems - 1) / kTargetItems;
+    tps = tps < 1 ? 1 : (tps > tiles ? tiles : tps);
+    int tiles_per_split = (int)tps;
+    if ((tiles + tiles_per_split - 1) / tiles_per_split > kMaxSplits) tiles_per_split = (tiles + kMaxSplits - 1) / kMaxSplits;
     // Split starts must be page aligned and a split's pages must fit in LDS.
     const int unit_tokens = page_size % TILE == 0 ? page_size : (TILE % page_size == 0 ? TILE : TILE * page_size);
     int split_tokens = tiles_per_split * TILE;
@@ -531,7 +584,7 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
     if (p.num_splits == 1) {
         p.part_o_bytes = p.part_ml_bytes = 0;
     } else {
-        p.part_o_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * D * sizeof(float));
+        p.part_o_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * D * sizeof(_Float16));
         p.part_ml_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * 2 * sizeof(float));
     }
     p.total = p.part_o_bytes + p.part_ml_bytes;
@@ -561,7 +614,7 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     if (MODE == kPacked && !vis) return D3D_E_NULL;
     const Plan pl = plan(B, Q, Hq, Hkv, max_context, page_size);
     if (!pl.valid) return D3D_E_UNSUPPORTED;
-    if ((int64_t)B * pl.nqt > 65535) return D3D_E_SHAPE;
+    if ((int64_t)B * pl.nqt > 65535 || (int64_t)B * pl.num_splits * Hkv > INT_MAX / 2) return D3D_E_SHAPE;
     if (pl.num_splits > 1 && (!workspace || ws_bytes < pl.total)) return D3D_E_WORKSPACE;
     Params P;
     P.q = static_cast<const uint16_t*>(q);
@@ -570,7 +623,7 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     P.block_table = block_table;
     P.context_lens = context_lens;
     P.out = static_cast<uint16_t*>(out);
-    P.part_o = pl.num_splits > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
+    P.part_o = pl.num_splits > 1 ? reinterpret_cast<_Float16*>(workspace) : nullptr;
     P.part_ml = pl.num_splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.part_o_bytes)
                                   : nullptr;
     P.B = B;
@@ -595,7 +648,8 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     P.num_splits = pl.num_splits;
     P.scale_log2 = scale * 1.4426950408889634f;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid(pl.num_splits, Hkv, B * pl.nqt);
+    // x = work item * Hkv + kv head; items past the requests' splits exit.
+    const dim3 grid(B * pl.num_splits * Hkv, pl.nqt);
     switch (pl.waves) {
         case 2:
             hipLaunchKernelGGL((attn_split_kernel<2, MODE>), grid, dim3(128), 0, s, P);
