@@ -186,8 +186,7 @@ __device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, fl
 
 template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
 __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowStat* lds, float* sM, float* sS,
-                                            int* sArg, uint8_t* sAcc, uint8_t* sBad, int* s_flags, float* rf,
-                                            int* ri) {
+                                            int* sArg, uint64_t* s_bits, float* rf, int* ri) {
     __shared__ float sQt[SP ? kMaxK : 1], sZ[SP ? kMaxK : 1];
     constexpr int E = Vec<DT>::E;
     const int K = P.K, V = P.V, C = P.C;
@@ -218,13 +217,15 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
     merge_rows<M, SP>(P, b, sM, sS, sArg, lds);
     if constexpr (SP) __syncthreads();
 
+    // Per-position decisions, then the first reject and the bad-token flag
+    // from wave ballots (positions 0..K-1 live in waves 0 and 1).
+    bool acc = false, badp = false;
     if (tid < K) {
-        const bool bad = tok < 0 || tok >= V;
-        bool acc = false;
+        badp = tok < 0 || tok >= V;
         if constexpr (M == kGreedy) {
-            acc = !bad && tok == (int64_t)sArg[tid];
+            acc = !badp && tok == (int64_t)sArg[tid];
         } else {
-            if (!bad) {
+            if (!badp) {
                 const float pt = prob_of<M, UNIT_T>(xt, sM[tid], inv_sum<M>(sS[tid]), P.T);
                 const float qt = SP ? sQt[tid]
                                     : prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
@@ -232,25 +233,21 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
                 acc = u <= a;
             }
         }
-        sAcc[tid] = acc;
-        sBad[tid] = bad;
     }
-    __syncthreads();
-    if (tid == 0) {
-        int n = K, bad = 0;
-        for (int p = 0; p < K; ++p) {
-            bad |= sBad[p];
-            if (!sAcc[p] && n == K) n = p;
+    {
+        const uint64_t rej = __ballot(tid < K && !acc);
+        const uint64_t bb = __ballot(badp);
+        const int wv = tid / kWave;
+        if ((tid & (kWave - 1)) == 0 && wv < 2) {
+            s_bits[wv] = rej;
+            s_bits[2 + wv] = bb;
         }
-        s_flags[0] = n;
-        s_flags[1] = bad;
     }
     __syncthreads();
-    const int n = s_flags[0];
-    const bool bad = s_flags[1] != 0;
-
+    const int n = s_bits[0] ? __builtin_ctzll(s_bits[0]) : (s_bits[1] ? 64 + __builtin_ctzll(s_bits[1]) : K);
+    const bool bad = (s_bits[2] | s_bits[3]) != 0;
     if (c == 0) {
-        for (int p = tid; p < K; p += NT) P.mask[(size_t)b * K + p] = sAcc[p];
+        for (int p = tid; p < K; p += NT) P.mask[(size_t)b * K + p] = acc;
         if (P.posterior)
             for (int r = tid; r <= K; r += NT) P.posterior[(size_t)b * (K + 1) + r] = sArg[r];
         if (tid == 0) {
@@ -328,11 +325,12 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
                 }
             }
         }
-        // One combined workgroup reduction for all sub-chunks.
+        // One combined workgroup reduction for the nv2 sub-chunks.
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
 #pragma unroll
             for (int j = 0; j < kMaxNv2; ++j) {
+                if (j >= nv2) break;
                 rs[j] += __shfl_xor(rs[j], o, kWave);
                 ps[j] += __shfl_xor(ps[j], o, kWave);
                 lr[j] = max(lr[j], __shfl_xor(lr[j], o, kWave));
@@ -364,16 +362,13 @@ __global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
     __shared__ RowStat lds[kMaxStatLds];
     __shared__ float sM[2 * kMaxK + 2], sS[2 * kMaxK + 2];
     __shared__ int sArg[kMaxK + 1];
-    __shared__ uint8_t sAcc[kMaxK + 1], sBad[kMaxK + 1];
-    __shared__ int s_flags[2];
+    __shared__ uint64_t s_bits[4];
     __shared__ float rf[NT / kWave];
     __shared__ int ri[NT / kWave];
     if (P.T == 1.0f)
-        decide_body<DT, VEC, M, true, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf,
-                                          ri);
+        decide_body<DT, VEC, M, true, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, s_bits, rf, ri);
     else
-        decide_body<DT, VEC, M, false, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, sAcc, sBad, s_flags, rf,
-                                           ri);
+        decide_body<DT, VEC, M, false, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, s_bits, rf, ri);
 }
 
 // ---------------------------------------------------------------- phase 3
@@ -396,9 +391,83 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
 
     // Chunk-level inverse CDF: inclusive scan of chunk sums in chunk order,
     // the crossing chunk is the first whose inclusive sum exceeds v * W.
-    // Pass 1 picks the weights (residual unless its mass is <= 1e-12).
+    // The weights are the residual unless its mass is <= 1e-12.
     float WR = 0.f, WP = 0.f;
     int LR = -1, LP = -1;
+    int cs = INT_MAX;
+    float base = 0.f;
+    bool use_r;
+    float W, target;
+    if (C <= NT) {
+        // One record per thread: both scans, both maxima and the crossing
+        // in two workgroup exchanges.
+        __shared__ float s_tot[2][NT / kWave];
+        __shared__ int s_max[2][NT / kWave];
+        __shared__ int s_first[NT / kWave];
+        __shared__ float s_base[NT / kWave];
+        const int lane = tid & (kWave - 1), wv = tid / kWave;
+        float ir = mine0.r, ip = mine0.p;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const float a = __shfl_up(ir, o, kWave), q = __shfl_up(ip, o, kWave);
+            if (lane >= o) {
+                ir += a;
+                ip += q;
+            }
+        }
+        const int mr = wave_max_int(mine0.last_r), mp = wave_max_int(mine0.last_p);
+        if (lane == kWave - 1) {
+            s_tot[0][wv] = ir;
+            s_tot[1][wv] = ip;
+        }
+        if (lane == 0) {
+            s_max[0][wv] = mr;
+            s_max[1][wv] = mp;
+        }
+        __syncthreads();
+        // Same arithmetic as block_incl_scan: wave scan + earlier waves' totals.
+        float orr = 0.f, orp = 0.f;
+        for (int k = 0; k < NT / kWave; ++k) {
+            if (k < wv) {
+                orr += s_tot[0][k];
+                orp += s_tot[1][k];
+            }
+            LR = max(LR, s_max[0][k]);
+            LP = max(LP, s_max[1][k]);
+        }
+        {
+            float offr = 0.f, offp = 0.f;
+            for (int k = 0; k < NT / kWave - 1; ++k) {
+                offr += s_tot[0][k];
+                offp += s_tot[1][k];
+            }
+            WR = s_tot[0][NT / kWave - 1] + offr;  // the scan's last element
+            WP = s_tot[1][NT / kWave - 1] + offp;
+        }
+        ir += orr;
+        ip += orp;
+        use_r = res && WR > 1e-12f;
+        W = use_r ? WR : WP;
+        target = v * W;
+        const float incl = use_r ? ir : ip, w = use_r ? mine0.r : mine0.p;
+        const uint64_t bal = __ballot(tid < C && incl > target);
+        if (bal && lane == __builtin_ctzll(bal)) {
+            s_first[wv] = tid;
+            s_base[wv] = incl - w;
+        }
+        if (!bal && lane == 0) s_first[wv] = INT_MAX;
+        __syncthreads();
+        for (int k = 0; k < NT / kWave; ++k)
+            if (s_first[k] != INT_MAX) {
+                cs = s_first[k];
+                base = s_base[k];
+                break;
+            }
+        if (!(W > 0.f)) {
+            if (tid == 0) P.out_token[b] = D3D_TOKEN_EMPTY_DISTRIBUTION;
+            return;
+        }
+    } else {
     for (int c0 = 0; c0 < C; c0 += NT) {
         float r = 0.f, p = 0.f;
         if (c0 + tid < C) {
@@ -421,15 +490,13 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
     }
     LR = block_max_int(LR, ri);
     LP = block_max_int(LP, ri);
-    const bool use_r = res && WR > 1e-12f;
-    const float W = use_r ? WR : WP;
-    const float target = v * W;
+    use_r = res && WR > 1e-12f;
+    W = use_r ? WR : WP;
+    target = v * W;
     if (!(W > 0.f)) {
         if (tid == 0) P.out_token[b] = D3D_TOKEN_EMPTY_DISTRIBUTION;
         return;
     }
-    int cs = INT_MAX;
-    float base = 0.f;
     float carry = 0.f;
     for (int c0 = 0; c0 < C && cs == INT_MAX; c0 += NT) {
         float w = 0.f;
@@ -449,6 +516,7 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
         }
         carry = s_f[3];
         __syncthreads();
+    }
     }
     int token;
     if (cs == INT_MAX) {

@@ -52,7 +52,13 @@ namespace attn {
 
 constexpr int D = 128;         // head dimension
 constexpr int TILE = 64;       // tokens per KV tile
-constexpr int ROWB = D * 2 + 16;  // LDS bytes per token row (16 B pad against bank conflicts)
+// LDS bytes per token row.  K rows are read 16 B per lane, 16 rows per
+// instruction: a 272-byte stride (68 banks) puts the 16 rows on 16 disjoint
+// 4-bank groups.  V rows are read 8 B per lane with 4 token rows (4 apart)
+// per wave: a 288-byte stride puts rows 4 apart 32 banks apart.
+constexpr int ROWB = D * 2 + 16;     // K
+constexpr int ROWB_V = D * 2 + 32;   // V
+constexpr int LDS_V = TILE * ROWB;   // V region offset
 constexpr int kMaxWaves = 8;   // up to 128 MFMA rows per workgroup
 constexpr int kMaxSplitPages = 1024;  // page ids staged per split
 
@@ -177,7 +183,7 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
         const int tl = (int)(threadIdx.x >> 4) + pss * (NT / 16);
         const bool ok = (okmask >> pss) & 1;
         *reinterpret_cast<u32x4*>(lds + tl * ROWB + seg * 16) = ok ? reg[pss] : z;
-        *reinterpret_cast<u32x4*>(lds + TILE * ROWB + tl * ROWB + seg * 16) = ok ? reg[NPASS + pss] : z;
+        *reinterpret_cast<u32x4*>(lds + LDS_V + tl * ROWB_V + seg * 16) = ok ? reg[NPASS + pss] : z;
     }
 }
 
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g4 = lane >> 4, c16 = lane & 15;
 
-    __shared__ __attribute__((aligned(16))) char lds[2 * TILE * ROWB];
+    __shared__ __attribute__((aligned(16))) char lds[TILE * (ROWB + ROWB_V)];
     __shared__ int pages[kMaxSplitPages];
     __shared__ int s_lim[2][NW];
 
@@ -279,7 +285,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     // One 64-token tile from LDS into the running (m, l, O) of each row.
     auto compute = [&](int t0) {
         const char* kl = lds;
-        const char* vl = lds + TILE * ROWB;
+        const char* vl = lds + LDS_V;
         // S^T sub-tiles: sc[m][r] = score of token t0 + 16m + 4*g4 + r for row c16.
         float sc[TILE / 16][4];
         {
@@ -298,10 +304,11 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
                     acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[m]), qop[ks], acc[m],
                                                                    0, 0, 0);
             }
+            // Raw scores; the softmax scale is applied inside the exponent.
 #pragma unroll
             for (int m = 0; m < TILE / 16; ++m)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[m][r] = acc[m][r] * P.scale_log2;
+                for (int r = 0; r < 4; ++r) sc[m][r] = acc[m][r];
         }
         // Masking only where the tile crosses the split end or the
         // visibility frontier of some row (a uniform test).
@@ -322,8 +329,9 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[m][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        // Rescale only when the running max of some row grows.
-        const float m_new = fmaxf(m_run, tmax);
+        // Rescale only when the running max of some row grows (log2 domain:
+        // scale * max raw score; the scale is positive, so the max commutes).
+        const float m_new = fmaxf(m_run, tmax * P.scale_log2);
         const bool grow = m_new > m_run;
         if (__any(grow)) {
             const float alpha = grow ? (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new)) : 1.f;
@@ -338,14 +346,17 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         }
         // P as the A operand of 16x16x32: sub-tiles 2mp and 2mp+1 give the
         // 8 token slots (4*g4 + r, then 16 + 4*g4 + r) of row c16.
+        // A row with no visible key so far has m_run = -inf and only -inf
+        // scores: exp2(-inf) = 0 with the offset taken as 0.
         uint32_t pw[TILE / 16][2];
         float psum = 0.f;
+        const float m_off = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
         for (int m = 0; m < TILE / 16; ++m) {
             float p[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                p[r] = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[m][r] - m_run);
+                p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[m][r], P.scale_log2, -m_off));
                 psum += p[r];
             }
             pw[m][0] = pack_bf16x2(p[0], p[1]);
@@ -363,7 +374,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int t = 32 * mp + 16 * (k >> 2) + 4 * g4 + (k & 3);
-                    vr[k] = *reinterpret_cast<const u32x2*>(vl + t * ROWB + (64 * h + 4 * c16) * 2);
+                    vr[k] = *reinterpret_cast<const u32x2*>(vl + t * ROWB_V + (64 * h + 4 * c16) * 2);
                 }
 #pragma unroll
                 for (int qq = 0; qq < 4; ++qq) {
@@ -553,7 +564,10 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Two workgroups are resident per CU (register-limited) on 256 CUs: 512 at
 // a time; about four rounds of work items keep the last round short.
-constexpr int kTargetItems = 2048;
+#ifndef D3D_ATTN_TARGET_ITEMS
+#define D3D_ATTN_TARGET_ITEMS 2048
+#endif
+constexpr int kTargetItems = D3D_ATTN_TARGET_ITEMS;
 
 static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
     Plan p;

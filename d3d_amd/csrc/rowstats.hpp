@@ -16,7 +16,7 @@ constexpr int kChunk = 4096;       // vocabulary entries per chunk
 constexpr int L = kChunk / NT;     // entries per thread per chunk
 constexpr int kMaxStatLds = 2048;  // RowStat entries staged in LDS per batch (32 KiB)
 
-struct RowStat {
+struct __attribute__((aligned(16))) RowStat {
     float m;     // max of z over the chunk (logits), 0 (probs)
     float s;     // sum exp(z - m) (logits) or sum x (probs)
     float xmax;  // max raw value
@@ -257,7 +257,22 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
         const int nr = min(batch_rows, rows - r0);
         const RowStat* src = stats + (size_t)r0 * C;
         __syncthreads();
-        for (int e = threadIdx.x; e < nr * C; e += NT) lds[e] = src[e];
+        // Up to kStage 16-byte records per thread in flight at once (loads
+        // past the end re-read the last record and are not stored).
+        constexpr int kStage = 8;
+        const int n = nr * C;
+        const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+        u32x4* l4 = reinterpret_cast<u32x4*>(lds);
+        for (int e0 = 0; e0 < n; e0 += NT * kStage) {
+            u32x4 t[kStage];
+#pragma unroll
+            for (int j = 0; j < kStage; ++j) t[j] = s4[min(e0 + j * NT + (int)threadIdx.x, n - 1)];
+#pragma unroll
+            for (int j = 0; j < kStage; ++j) {
+                const int e = e0 + j * NT + threadIdx.x;
+                if (e < n) l4[e] = t[j];
+            }
+        }
         __syncthreads();
         for (int rr0 = 0; rr0 < nr; rr0 += kRowsPerPass) {
             const int rr = rr0 + threadIdx.x / kLanesPerRow;
