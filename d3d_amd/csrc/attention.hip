@@ -59,6 +59,9 @@ constexpr int TILE = 64;       // tokens per KV tile
 constexpr int ROWB = D * 2 + 16;     // K
 constexpr int ROWB_V = D * 2 + 32;   // V
 constexpr int LDS_V = TILE * ROWB;   // V region offset
+#ifndef D3D_ATTN_DEPTH
+#define D3D_ATTN_DEPTH 1
+#endif
 constexpr int kMaxWaves = 8;   // up to 128 MFMA rows per workgroup
 constexpr int kMaxSplitPages = 1024;  // page ids staged per split
 
@@ -393,8 +396,10 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     };
 
     // Tiles are staged global -> registers -> LDS; DEPTH register sets keep
-    // that many tiles in flight while the current one is computed.
-    constexpr int DEPTH = NW == 4 ? 2 : 1;
+    // that many tiles in flight while the current one is computed (one set
+    // measured faster than two: the second set's 64 VGPRs cost a wave per
+    // SIMD).
+    constexpr int DEPTH = NW == 4 ? D3D_ATTN_DEPTH : 1;
     u32x4 regA[2 * TILE * 16 / NT];
     int okA = 0;
     if (t_begin < t_end) fetch_tile<NT>(P, kvh, t_begin, t_begin, t_end, pages, safe_row, regA, okA);

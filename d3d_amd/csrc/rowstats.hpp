@@ -12,7 +12,10 @@ namespace d3d {
 namespace rows {
 
 constexpr int NT = 256;            // threads per workgroup (4 waves)
-constexpr int kChunk = 4096;       // vocabulary entries per chunk
+#ifndef D3D_ROWS_CHUNK
+#define D3D_ROWS_CHUNK 4096
+#endif
+constexpr int kChunk = D3D_ROWS_CHUNK;  // vocabulary entries per chunk
 constexpr int L = kChunk / NT;     // entries per thread per chunk
 constexpr int kMaxStatLds = 2048;  // RowStat entries staged in LDS per batch (32 KiB)
 
@@ -280,6 +283,7 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
             float m = -INFINITY, xm = -INFINITY;
             int am = INT_MAX;
             if (live) {
+#pragma unroll 4
                 for (int k = g; k < C; k += kLanesPerRow) {
                     const RowStat t = lds[rr * C + k];
                     m = fmaxf(m, t.m);
@@ -295,6 +299,7 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
             }
             float s = 0.f;
             if (live && M != kGreedy) {
+#pragma unroll 4
                 for (int k = g; k < C; k += kLanesPerRow) {
                     const RowStat t = lds[rr * C + k];
                     if constexpr (M == kProbs) {

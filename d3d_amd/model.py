@@ -264,6 +264,13 @@ class BlockStep:
         self.lens.copy_(lens, non_blocking=True)
 
     def __call__(self, ids, pos, tables, slots, lens):
+        # Always under inference mode: torch keeps per-generator graph state
+        # tensors that a first capture creates, and a later capture outside
+        # the mode they were created in cannot update them in place.
+        with torch.inference_mode():
+            return self._call(ids, pos, tables, slots, lens)
+
+    def _call(self, ids, pos, tables, slots, lens):
         self._load(ids, pos, tables, slots, lens)
         if not self.use_graph:
             return self._body()
