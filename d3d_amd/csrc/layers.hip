@@ -42,6 +42,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
     __shared__ float red[NT / kWave];
     constexpr int kMaxVec = 4;  // up to 4 vectors of 8 per thread: H <= 8192
     float v[kMaxVec][8];
+    u32x4 wreg[kMaxVec];  // the weights load with the row, not after the reduction
     const int nvec = H / 8;
     float ss = 0.f;
 #pragma unroll
@@ -49,6 +50,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
         const int vi = threadIdx.x + j * NT;
         if (vi >= nvec) break;
         const size_t off = row * H + vi * 8;
+        wreg[j] = *reinterpret_cast<const u32x4*>(w + vi * 8);
         const u32x4 r = *reinterpret_cast<const u32x4*>(residual + off);
         u32x4 a = {0u, 0u, 0u, 0u};
         if (x) a = *reinterpret_cast<const u32x4*>(x + off);
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
         const int vi = threadIdx.x + j * NT;
         if (vi >= nvec) break;
         const size_t off = row * H + vi * 8;
-        const u32x4 wv = *reinterpret_cast<const u32x4*>(w + vi * 8);
+        const u32x4 wv = wreg[j];
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
@@ -88,63 +90,77 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
 
 // One workgroup per token; wave w handles heads w, w + 4, ...: query heads
 // (norm + rope -> q_out), key heads (norm + rope -> k_cache) and value heads
-// (copy -> v_cache).
+// (copy -> v_cache).  Lane l holds entries l and l + 64 of a head, the pair
+// the rotate-half RoPE mixes, and computes that pair's cos / sin itself.
 template <bool DRAFT_ROPE>
 __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
     const uint16_t* __restrict__ qkv, const int64_t* __restrict__ positions, const uint16_t* __restrict__ qn,
     const uint16_t* __restrict__ kn, const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out,
     uint16_t* k_cache, uint16_t* v_cache, const int64_t* __restrict__ slots, int Hq, int Hkv, float eps,
     int64_t num_slots) {
+    constexpr int WAVES = NT / kWave;
+    constexpr int HPW = 16;  // heads per wave whose loads are in flight together
     const size_t t = blockIdx.x;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    __shared__ float cs[HD / 2], sn[HD / 2];
-    const int64_t pos = positions[t];
-    if (threadIdx.x < HD / 2) {
-        const float f = (float)pos * inv_freq[threadIdx.x];
-        cs[threadIdx.x] = cosf(f);
-        sn[threadIdx.x] = sinf(f);
-    }
-    __syncthreads();
-    const int64_t slot = slots[t];
-    const bool store = slot >= 0 && slot < num_slots;
-    const uint16_t* row = qkv + t * (size_t)(Hq + 2 * Hkv) * HD;
     const int heads = Hq + 2 * Hkv;
-    for (int h = wv; h < heads; h += NT / kWave) {
-        const uint16_t* src = row + (size_t)h * HD;
-        const uint16_t a = src[lane], b = src[lane + 64];
-        if (h >= Hq + Hkv) {  // value head: copy into the cache
-            if (store) {
-                uint16_t* dst = v_cache + ((size_t)slot * Hkv + (h - Hq - Hkv)) * HD;
-                dst[lane] = a;
-                dst[lane + 64] = b;
+    const uint16_t* row = qkv + t * (size_t)heads * HD;
+    // Every independent load first: the position, the slot, the norm
+    // weights of this lane's two entries and the first HPW heads of this wave.
+    const int64_t pos = positions[t];
+    const int64_t slot = slots[t];
+    const float fq = inv_freq[lane];
+    const float qn0 = bf(qn[lane]), qn1 = bf(qn[lane + 64]);
+    const float kn0 = bf(kn[lane]), kn1 = bf(kn[lane + 64]);
+    const bool store = slot >= 0 && slot < num_slots;
+    for (int base = 0; base < heads; base += WAVES * HPW) {
+        uint16_t a[HPW], b[HPW];
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) {
+            const int h = base + wv + j * WAVES;
+            if (h < heads) {
+                a[j] = row[(size_t)h * HD + lane];
+                b[j] = row[(size_t)h * HD + lane + 64];
             }
-            continue;
         }
-        const bool is_q = h < Hq;
-        const float x0 = bf(a), x1 = bf(b);
-        const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
-        const uint16_t* nw = is_q ? qn : kn;
-        const float y0 = rbf(rbf(x0 * rstd) * bf(nw[lane]));
-        const float y1 = rbf(rbf(x1 * rstd) * bf(nw[lane + 64]));
-        float o0, o1;
-        if constexpr (DRAFT_ROPE) {
-            const float c = rbf(cs[lane]), s = rbf(sn[lane]);
-            o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
-            o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
-        } else {
-            const float c = cs[lane], s = sn[lane];
-            o0 = y0 * c - y1 * s;
-            o1 = y1 * c + y0 * s;
+        // cos / sin of this lane's frequency (entries lane and lane + 64).
+        const float f = (float)pos * fq;
+        const float cs = cosf(f), sn = sinf(f);
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) {
+            const int h = base + wv + j * WAVES;
+            if (h >= heads) break;
+            if (h >= Hq + Hkv) {  // value head: copy into the cache
+                if (store) {
+                    uint16_t* dst = v_cache + ((size_t)slot * Hkv + (h - Hq - Hkv)) * HD;
+                    dst[lane] = a[j];
+                    dst[lane + 64] = b[j];
+                }
+                continue;
+            }
+            const bool is_q = h < Hq;
+            const float x0 = bf(a[j]), x1 = bf(b[j]);
+            const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
+            const float y0 = rbf(rbf(x0 * rstd) * (is_q ? qn0 : kn0));
+            const float y1 = rbf(rbf(x1 * rstd) * (is_q ? qn1 : kn1));
+            float o0, o1;
+            if constexpr (DRAFT_ROPE) {
+                const float c = rbf(cs), s = rbf(sn);
+                o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
+                o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
+            } else {
+                o0 = y0 * cs - y1 * sn;
+                o1 = y1 * cs + y0 * sn;
+            }
+            uint16_t* dst;
+            if (is_q) {
+                dst = q_out + (t * Hq + h) * HD;
+            } else {
+                if (!store) continue;
+                dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
+            }
+            dst[lane] = f32_to_bf16_bits(o0);
+            dst[lane + 64] = f32_to_bf16_bits(o1);
         }
-        uint16_t* dst;
-        if (is_q) {
-            dst = q_out + (t * Hq + h) * HD;
-        } else {
-            if (!store) continue;
-            dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
-        }
-        dst[lane] = f32_to_bf16_bits(o0);
-        dst[lane + 64] = f32_to_bf16_bits(o1);
     }
 }
 
