@@ -88,7 +88,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
     }
 }
 
-// One workgroup per token; wave w handles heads w, w + 4, ...: query heads
+// One wave per (token, head): grid (tokens, ceil(heads / 4)).  Query heads
 // (norm + rope -> q_out), key heads (norm + rope -> k_cache) and value heads
 // (copy -> v_cache).  Lane l holds entries l and l + 64 of a head, the pair
 // the rotate-half RoPE mixes, and computes that pair's cos / sin itself.
@@ -98,70 +98,53 @@ __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
     const uint16_t* __restrict__ kn, const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out,
     uint16_t* k_cache, uint16_t* v_cache, const int64_t* __restrict__ slots, int Hq, int Hkv, float eps,
     int64_t num_slots) {
-    constexpr int WAVES = NT / kWave;
-    constexpr int HPW = 16;  // heads per wave whose loads are in flight together
     const size_t t = blockIdx.x;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int h = blockIdx.y * (NT / kWave) + (threadIdx.x >> 6);
     const int heads = Hq + 2 * Hkv;
-    const uint16_t* row = qkv + t * (size_t)heads * HD;
-    // Every independent load first: the position, the slot, the norm
-    // weights of this lane's two entries and the first HPW heads of this wave.
-    const int64_t pos = positions[t];
+    if (h >= heads) return;  // whole wave; no barrier in this kernel
+    const uint16_t* src = qkv + (t * (size_t)heads + h) * HD;
+    // Every load of this wave at once.
+    const uint16_t a = src[lane], b = src[lane + 64];
     const int64_t slot = slots[t];
-    const float fq = inv_freq[lane];
-    const float qn0 = bf(qn[lane]), qn1 = bf(qn[lane + 64]);
-    const float kn0 = bf(kn[lane]), kn1 = bf(kn[lane + 64]);
     const bool store = slot >= 0 && slot < num_slots;
-    for (int base = 0; base < heads; base += WAVES * HPW) {
-        uint16_t a[HPW], b[HPW];
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-            const int h = base + wv + j * WAVES;
-            if (h < heads) {
-                a[j] = row[(size_t)h * HD + lane];
-                b[j] = row[(size_t)h * HD + lane + 64];
-            }
+    if (h >= Hq + Hkv) {  // value head: copy into the cache
+        if (store) {
+            uint16_t* dst = v_cache + ((size_t)slot * Hkv + (h - Hq - Hkv)) * HD;
+            dst[lane] = a;
+            dst[lane + 64] = b;
         }
-        // cos / sin of this lane's frequency (entries lane and lane + 64).
-        const float f = (float)pos * fq;
-        const float cs = cosf(f), sn = sinf(f);
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-            const int h = base + wv + j * WAVES;
-            if (h >= heads) break;
-            if (h >= Hq + Hkv) {  // value head: copy into the cache
-                if (store) {
-                    uint16_t* dst = v_cache + ((size_t)slot * Hkv + (h - Hq - Hkv)) * HD;
-                    dst[lane] = a[j];
-                    dst[lane + 64] = b[j];
-                }
-                continue;
-            }
-            const bool is_q = h < Hq;
-            const float x0 = bf(a[j]), x1 = bf(b[j]);
-            const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
-            const float y0 = rbf(rbf(x0 * rstd) * (is_q ? qn0 : kn0));
-            const float y1 = rbf(rbf(x1 * rstd) * (is_q ? qn1 : kn1));
-            float o0, o1;
-            if constexpr (DRAFT_ROPE) {
-                const float c = rbf(cs), s = rbf(sn);
-                o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
-                o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
-            } else {
-                o0 = y0 * cs - y1 * sn;
-                o1 = y1 * cs + y0 * sn;
-            }
-            uint16_t* dst;
-            if (is_q) {
-                dst = q_out + (t * Hq + h) * HD;
-            } else {
-                if (!store) continue;
-                dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
-            }
-            dst[lane] = f32_to_bf16_bits(o0);
-            dst[lane + 64] = f32_to_bf16_bits(o1);
-        }
+        return;
     }
+    const bool is_q = h < Hq;
+    const uint16_t* nw = is_q ? qn : kn;
+    const float w0 = bf(nw[lane]), w1 = bf(nw[lane + 64]);
+    const int64_t pos = positions[t];
+    const float f = (float)pos * inv_freq[lane];
+    const float x0 = bf(a), x1 = bf(b);
+    const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
+    const float y0 = rbf(rbf(x0 * rstd) * w0);
+    const float y1 = rbf(rbf(x1 * rstd) * w1);
+    // cos / sin of this lane's frequency (entries lane and lane + 64).
+    const float cs = cosf(f), sn = sinf(f);
+    float o0, o1;
+    if constexpr (DRAFT_ROPE) {
+        const float c = rbf(cs), s = rbf(sn);
+        o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
+        o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
+    } else {
+        o0 = y0 * cs - y1 * sn;
+        o1 = y1 * cs + y0 * sn;
+    }
+    uint16_t* dst;
+    if (is_q) {
+        dst = q_out + (t * Hq + h) * HD;
+    } else {
+        if (!store) return;
+        dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
+    }
+    dst[lane] = f32_to_bf16_bits(o0);
+    dst[lane + 64] = f32_to_bf16_bits(o1);
 }
 
 // out[t, i] = silu(gate[t, i]) * up[t, i] with gate_up = [gate | up] per row.
@@ -217,13 +200,14 @@ extern "C" int d3d_qk_rope_append(const void* qkv, const int64_t* positions, con
         return D3D_E_NULL;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const auto* a = static_cast<const uint16_t*>(qkv);
+    const dim3 grid(T, (Hq + 2 * Hkv + layers::NT / kWave - 1) / (layers::NT / kWave));
     if (draft_rope)
-        hipLaunchKernelGGL(layers::qk_rope_append_kernel<true>, dim3(T), dim3(layers::NT), 0, s, a, positions,
+        hipLaunchKernelGGL(layers::qk_rope_append_kernel<true>, grid, dim3(layers::NT), 0, s, a, positions,
                            static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
                            inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
                            static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
     else
-        hipLaunchKernelGGL(layers::qk_rope_append_kernel<false>, dim3(T), dim3(layers::NT), 0, s, a, positions,
+        hipLaunchKernelGGL(layers::qk_rope_append_kernel<false>, grid, dim3(layers::NT), 0, s, a, positions,
                            static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
                            inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
                            static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
