@@ -13,7 +13,7 @@
 // (single/eval_sync.py:763-768, torch.topk of log_softmax: the same ids).
 //
 // Two kernels: (1) grid (chunks, rows): each workgroup takes k rounds of a
-// workgroup argmax over its 16384-entry chunk (each thread holds 64 entries
+// workgroup argmax over its 4096-entry chunk (each thread holds 16 entries
 // in registers and excludes the ones already taken) and writes k (value,
 // index) candidates; (2) one workgroup per row merges the chunk candidates
 // the same way.  Streaming the logits once is the HBM-bound part.
@@ -30,10 +30,6 @@ using namespace rows;
 
 constexpr int kMaxK = 64;
 constexpr int kMaxCand = 8192;  // chunk candidates per row merged in LDS
-// Entries per thread and per chunk: 64 x 256 = 16384 entries per workgroup
-// (a wide chunk keeps the workgroup count low for many short rows).
-constexpr int TL = 64;
-constexpr int kTopkChunk = NT * TL;
 
 struct Cand {
     float v;
@@ -56,15 +52,15 @@ __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
     __shared__ float sv[NT / kWave];
     __shared__ int si[NT / kWave];
     const void* row = row_ptr<DT>(P.logits, n, P.V);
-    const int first = c * kTopkChunk + threadIdx.x * E;
-    float x[TL];
-    load_tile<DT, VEC, true, TL>(row, P.V, first, NT * E, -INFINITY, x);
-    uint64_t taken = 0;  // bit l: entry l already selected
+    const int first = c * kChunk + threadIdx.x * E;
+    float x[L];
+    load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
+    uint32_t taken = 0;  // bit l: entry l already selected
     for (int r = 0; r < P.k; ++r) {
         float bv = -INFINITY;
         int bi = INT_MAX;
 #pragma unroll
-        for (int l = 0; l < TL; ++l) {
+        for (int l = 0; l < L; ++l) {
             const int e = tile_index<DT>(first, NT * E, l);
             if (!((taken >> l) & 1u) && e < P.V) argmax_merge(bv, bi, x[l], e);
         }
@@ -73,15 +69,15 @@ __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
         block_argmax<NT>(wv, wi, sv, si);
         // The owner of the winning entry excludes it from later rounds.
 #pragma unroll
-        for (int l = 0; l < TL; ++l)
-            if (tile_index<DT>(first, NT * E, l) == wi) taken |= (uint64_t)1 << l;
+        for (int l = 0; l < L; ++l)
+            if (tile_index<DT>(first, NT * E, l) == wi) taken |= 1u << l;
         if (threadIdx.x == 0) P.cand[((size_t)n * P.C + c) * P.k + r] = Cand{wv, wi};
         if (r == 0 && P.lse) {
             // Round 0's winner is the chunk max: the chunk's share of logsumexp.
             float se = 0.f;
             if (wv != -INFINITY) {
 #pragma unroll
-                for (int l = 0; l < TL; ++l)
+                for (int l = 0; l < L; ++l)
                     if (tile_index<DT>(first, NT * E, l) < P.V) se += expf(x[l] - wv);
             }
             se = block_sum<NT>(se, sv);
@@ -142,13 +138,13 @@ __global__ __launch_bounds__(NT) void topk_merge_kernel(Params P) {
 using namespace d3d;
 
 static size_t cand_bytes(int N, int64_t V, int k) {
-    const size_t C = (size_t)((V + topk::kTopkChunk - 1) / topk::kTopkChunk);
+    const size_t C = (size_t)((V + rows::kChunk - 1) / rows::kChunk);
     return ((size_t)N * C * k * sizeof(topk::Cand) + 255) & ~(size_t)255;
 }
 
 extern "C" size_t d3d_topk_workspace_bytes(int N, int64_t V, int k) {
     if (N < 1 || V < 1 || k < 1) return 0;
-    const size_t C = (size_t)((V + topk::kTopkChunk - 1) / topk::kTopkChunk);
+    const size_t C = (size_t)((V + rows::kChunk - 1) / rows::kChunk);
     return cand_bytes(N, V, k) + (((size_t)N * C * sizeof(float2) + 255) & ~(size_t)255);
 }
 
@@ -165,7 +161,7 @@ extern "C" int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, in
     P.logits = logits;
     P.N = N;
     P.V = (int)V;
-    P.C = (int)((V + topk::kTopkChunk - 1) / topk::kTopkChunk);
+    P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
     P.k = k;
     if ((int64_t)P.C * k > kMaxCand) return D3D_E_SHAPE;
     if (workspace_bytes < d3d_topk_workspace_bytes(N, V, k)) return D3D_E_WORKSPACE;
