@@ -31,6 +31,14 @@ import torch
 
 HBM_PEAK_GBPS = 8000.0
 
+# HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# (two passes of `bench.py --no-cpu-baseline --no-models --calibrate-copy`),
+# each counter scaled by what it reads for a plain 64 MiB device copy in the
+# same process: FETCH_SIZE x 1.99920, WRITE_SIZE x 1.0.  They are measured
+# figures, not computed here; a kernel change needs a new counter pass.
+TRAFFIC_ACCEPT_B1 = 20_635_812      # stats + decide + resample, 1.095 x algorithmic
+TRAFFIC_VERIFY_ATTN_B1 = 18_019_285  # split + combine, 2.07 x algorithmic (fp16 partials)
+
 
 def _parse():
     ap = argparse.ArgumentParser()
@@ -252,10 +260,10 @@ def main():
     # The dominant kernel is the acceptance call when it takes longer.
     if acc_ms >= attn_ms:
         roof = {"bound": "hbm", "achieved": round(acc_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(acc_gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "fused acceptance"}
+                "frac": round(acc_gbps / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_ACCEPT_B1, "kernel": "fused acceptance"}
     else:
         roof = {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "verify attention"}
+                "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_VERIFY_ATTN_B1, "kernel": "verify attention"}
 
     # Secondary figures: greedy acceptance, batch-8 acceptance, batch-8
     # concurrent verify attention, batch-4 draft block attention.
