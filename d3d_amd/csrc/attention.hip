@@ -176,11 +176,57 @@ __device__ __forceinline__ void fetch_tile(const Params& P, int kvh, int t0, int
     }
 }
 
+// Wave-uniform variant for power-of-two pages of at least 4 tokens.  A
+// wave's 64 lanes cover 4 consecutive token rows starting at a multiple of 4
+// (tiles start at page- and 64-aligned split offsets), so the 4 rows share
+// one page: the page id and the rows' base address are scalar, and each lane
+// adds a fixed 32-bit offset (row in the group, KV head, 16-byte segment).
 template <int NT>
-__device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TILE * 16 / NT], int okmask) {
+__device__ __forceinline__ void fetch_tile_u(const Params& P, int t0, int t_begin, int t_end, const int* pages,
+                                             int safe_row, uint32_t lane_off, u32x4 (&reg)[2 * TILE * 16 / NT],
+                                             int& okmask) {
+    constexpr int NPASS = TILE * 16 / NT;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int rl = (int)(threadIdx.x >> 4) & 3;
+    const size_t row_bytes = (size_t)P.Hkv * D * 2;
+    int pg[NPASS];
+#pragma unroll
+    for (int pss = 0; pss < NPASS; ++pss) {
+        const int tw = t0 + 4 * w + pss * (NT / 16);
+        pg[pss] = tw < t_end ? pages[(tw - t_begin) >> P.page_shift] : -1;  // index inside the split
+    }
+    okmask = 0;
+#pragma unroll
+    for (int pss = 0; pss < NPASS; ++pss) {
+        const int tw = t0 + 4 * w + pss * (NT / 16);
+        const int page = __builtin_amdgcn_readfirstlane(pg[pss]);
+        const bool pok = page >= 0 && page < P.num_pages;
+        const int base = pok ? page * P.page_size + (tw & (P.page_size - 1)) : safe_row;
+        const char* kb = reinterpret_cast<const char*>(P.k_cache) + (size_t)base * row_bytes;
+        const char* vb = reinterpret_cast<const char*>(P.v_cache) + (size_t)base * row_bytes;
+        reg[pss] = *reinterpret_cast<const u32x4*>(kb + lane_off);
+        reg[NPASS + pss] = *reinterpret_cast<const u32x4*>(vb + lane_off);
+        okmask |= (int)(pok && tw + rl < t_end) << pss;
+    }
+}
+
+// clean: every row of the tile is live and on an in-pool page (uniform), so
+// no row needs zeroing.
+template <int NT>
+__device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TILE * 16 / NT], int okmask,
+                                           bool clean) {
     constexpr int NPASS = TILE * 16 / NT;
     const int seg = threadIdx.x & 15;
     const u32x4 z = {0u, 0u, 0u, 0u};
+    if (clean) {
+#pragma unroll
+        for (int pss = 0; pss < NPASS; ++pss) {
+            const int tl = (int)(threadIdx.x >> 4) + pss * (NT / 16);
+            *reinterpret_cast<u32x4*>(lds + tl * ROWB + seg * 16) = reg[pss];
+            *reinterpret_cast<u32x4*>(lds + LDS_V + tl * ROWB_V + seg * 16) = reg[NPASS + pss];
+        }
+        return;
+    }
 #pragma unroll
     for (int pss = 0; pss < NPASS; ++pss) {
         const int tl = (int)(threadIdx.x >> 4) + pss * (NT / 16);
@@ -192,7 +238,8 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
 
 // Register budget: two workgroups per CU (two waves per SIMD) so that each
 // CU keeps 2 x DEPTH tiles of K/V in flight.
-template <int NW, int MODE>
+// UPG: pages are a power of two of at least 4 tokens (wave-uniform page ids).
+template <int NW, int MODE, bool UPG>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
     constexpr int NT = NW * 64;
     const int kvh = blockIdx.x % P.Hkv, qt = blockIdx.y;
@@ -256,16 +303,32 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     // Page ids of the whole split in one round trip (split starts are page aligned).
     const int p0 = t_begin / P.page_size;
     const int np = t_end > t_begin ? (t_end - 1) / P.page_size - p0 + 1 : 0;
-    for (int i = threadIdx.x; i < np; i += NT) pages[i] = P.block_table[(size_t)b * P.max_pages + p0 + i];
-    __syncthreads();
+    int bad_page = 0;
+    for (int i = threadIdx.x; i < np; i += NT) {
+        const int pg = P.block_table[(size_t)b * P.max_pages + p0 + i];
+        pages[i] = pg;
+        bad_page |= pg < 0 || pg >= P.num_pages;
+    }
+    const bool pages_ok = !__syncthreads_or(bad_page);
     // A row every masked lane may read: the first in-pool page of the split
     // (or cache row 0).
-    size_t safe_row = 0;
+    int safe_row = 0;
     for (int i = 0; i < np; ++i)
         if (pages[i] >= 0 && pages[i] < P.num_pages) {
-            safe_row = (size_t)pages[i] * P.page_size;
+            safe_row = pages[i] * P.page_size;
             break;
         }
+    const uint32_t lane_off = (uint32_t)(((threadIdx.x >> 4) & 3) * P.Hkv * D * 2 + kvh * D * 2 + (threadIdx.x & 15) * 16);
+    // Stage tokens [t0, t0 + TILE) into registers / store them to LDS.
+    auto fetch = [&](int t0, u32x4 (&reg)[2 * TILE * 16 / NT], int& ok) {
+        if constexpr (UPG)
+            fetch_tile_u<NT>(P, t0, t_begin, t_end, pages, safe_row, lane_off, reg, ok);
+        else
+            fetch_tile<NT>(P, kvh, t0, t_begin, t_end, pages, (size_t)safe_row, reg, ok);
+    };
+    auto store = [&](int t0, const u32x4 (&reg)[2 * TILE * 16 / NT], int ok) {
+        store_tile<NT>(lds, reg, ok, pages_ok && t0 + TILE <= t_end);
+    };
 
 
     // Q^T operand of v_mfma_f32_16x16x32_bf16: lane l holds row l%16, head
@@ -402,33 +465,46 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     constexpr int DEPTH = NW == 4 ? D3D_ATTN_DEPTH : 1;
     u32x4 regA[2 * TILE * 16 / NT];
     int okA = 0;
-    if (t_begin < t_end) fetch_tile<NT>(P, kvh, t_begin, t_begin, t_end, pages, safe_row, regA, okA);
+    if (t_begin < t_end) fetch(t_begin, regA, okA);
     if constexpr (DEPTH == 1) {
-        for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
+        // Whole tiles on in-pool pages store without zeroing; the split's
+        // partial last tile (and every tile of a split that names an
+        // out-of-pool page) zeroes its dead rows.  Two loops rather than a
+        // per-tile branch: with the branch inside one loop the compiler
+        // waits for the next tile's loads before the first MFMA.
+        int t0 = t_begin;
+        if (pages_ok) {
+            for (; t0 + TILE <= t_end; t0 += TILE) {
+                __syncthreads();
+                store_tile<NT>(lds, regA, okA, true);
+                __syncthreads();
+                if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
+                compute(t0);
+            }
+        }
+        for (; t0 < t_end; t0 += TILE) {
             __syncthreads();
-            store_tile<NT>(lds, regA, okA);
+            store_tile<NT>(lds, regA, okA, false);
             __syncthreads();
-            if (t0 + TILE < t_end) fetch_tile<NT>(P, kvh, t0 + TILE, t_begin, t_end, pages, safe_row, regA, okA);
+            if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
             compute(t0);
         }
     } else {
         u32x4 regB[2 * TILE * 16 / NT];
         int okB = 0;
         if (t_begin + TILE < t_end)
-            fetch_tile<NT>(P, kvh, t_begin + TILE, t_begin, t_end, pages, safe_row, regB, okB);
+            fetch(t_begin + TILE, regB, okB);
         for (int t0 = t_begin; t0 < t_end; t0 += 2 * TILE) {
             __syncthreads();
-            store_tile<NT>(lds, regA, okA);
+            store(t0, regA, okA);
             __syncthreads();
-            if (t0 + 2 * TILE < t_end)
-                fetch_tile<NT>(P, kvh, t0 + 2 * TILE, t_begin, t_end, pages, safe_row, regA, okA);
+            if (t0 + 2 * TILE < t_end) fetch(t0 + 2 * TILE, regA, okA);
             compute(t0);
             if (t0 + TILE < t_end) {
                 __syncthreads();
-                store_tile<NT>(lds, regB, okB);
+                store(t0 + TILE, regB, okB);
                 __syncthreads();
-                if (t0 + 3 * TILE < t_end)
-                    fetch_tile<NT>(P, kvh, t0 + 3 * TILE, t_begin, t_end, pages, safe_row, regB, okB);
+                if (t0 + 3 * TILE < t_end) fetch(t0 + 3 * TILE, regB, okB);
                 compute(t0 + TILE);
             }
         }
@@ -669,15 +745,26 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     hipStream_t s = static_cast<hipStream_t>(stream);
     // x = work item * Hkv + kv head; items past the requests' splits exit.
     const dim3 grid(B * pl.num_splits * Hkv, pl.nqt);
+    // Power-of-two pages of at least 4 tokens take the wave-uniform fetch.
+    const bool upg = P.page_shift >= 2;
     switch (pl.waves) {
         case 2:
-            hipLaunchKernelGGL((attn_split_kernel<2, MODE>), grid, dim3(128), 0, s, P);
+            if (upg)
+                hipLaunchKernelGGL((attn_split_kernel<2, MODE, true>), grid, dim3(128), 0, s, P);
+            else
+                hipLaunchKernelGGL((attn_split_kernel<2, MODE, false>), grid, dim3(128), 0, s, P);
             break;
         case 4:
-            hipLaunchKernelGGL((attn_split_kernel<4, MODE>), grid, dim3(256), 0, s, P);
+            if (upg)
+                hipLaunchKernelGGL((attn_split_kernel<4, MODE, true>), grid, dim3(256), 0, s, P);
+            else
+                hipLaunchKernelGGL((attn_split_kernel<4, MODE, false>), grid, dim3(256), 0, s, P);
             break;
         default:
-            hipLaunchKernelGGL((attn_split_kernel<8, MODE>), grid, dim3(512), 0, s, P);
+            if (upg)
+                hipLaunchKernelGGL((attn_split_kernel<8, MODE, true>), grid, dim3(512), 0, s, P);
+            else
+                hipLaunchKernelGGL((attn_split_kernel<8, MODE, false>), grid, dim3(512), 0, s, P);
             break;
     }
     if (pl.num_splits > 1)
