@@ -172,6 +172,23 @@ def draft_block_bench(dev, reps: int = 20):
     return ms
 
 
+def lmhead_bench(dev, steps: int, warmup: int):
+    """Fused LM head + top-2 (the draft recovery block: 64 hidden rows, H 2048,
+    V 151936, random bf16 weights) against the unfused bf16 GEMM + top-k."""
+    from d3d_amd.draft import topk_tokens
+    from d3d_amd.lmhead import lmhead_topk
+    g = torch.Generator().manual_seed(3)
+    T, H, V = 64, 2048, 151936
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    fused = time_calls(lambda: lmhead_topk(x, w, 2), steps, warmup, dev)
+    unfused = time_calls(lambda: topk_tokens(torch.nn.functional.linear(x, w), 2), steps, warmup, dev)
+    nbytes = V * H * 2 + T * H * 2
+    del x, w
+    torch.cuda.empty_cache()
+    return fused, unfused, nbytes
+
+
 def e2e_bench(dev, new_tokens: int):
     """Qwen3-8B-shaped target + Qwen3-1.7B-shaped draft co-resident, two streams:
     batch 4, prompts of 512 random ids, greedy, 16-token blocks, 16-token pages."""
@@ -315,6 +332,10 @@ def main():
         "draft_attn_b4_us": round(dr_ms * 1e3, 2),
         "draft_attn_b4_gbps": round(dr.bytes / (dr_ms * 1e-3) / 1e9, 1),
     }
+    lm_ms, lm_unfused_ms, lm_bytes = lmhead_bench(dev, min(args.steps, 100), min(args.warmup, 10))
+    out["lmhead_top2_t64_us"] = round(lm_ms * 1e3, 2)
+    out["lmhead_top2_t64_gbps"] = round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1)
+    out["lmhead_gemm_then_topk_t64_us"] = round(lm_unfused_ms * 1e3, 2)
     if not args.no_models:
         out["draft_block_step_ms"] = round(draft_block_bench(dev), 3)
         res = e2e_bench(dev, args.e2e_new_tokens)

@@ -189,7 +189,7 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
                                             int* sArg, uint64_t* s_bits, float* rf, int* ri) {
     __shared__ float sQt[SP ? kMaxK : 1], sZ[SP ? kMaxK : 1];
     constexpr int E = Vec<DT>::E;
-    const int K = P.K, V = P.V, C = P.C;
+    const int K = P.K, V = P.V;
     const int tid = threadIdx.x;
 
     // Independent loads first: tokens, uniforms and token values.

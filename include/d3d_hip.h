@@ -257,6 +257,29 @@ int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int lo
                   int64_t* ids_out, float* vals_out, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* Bytes of workspace d3d_lmhead_topk needs. */
+size_t d3d_lmhead_workspace_bytes(int T, int64_t V, int k);
+
+/*
+ * Fused LM head + top-k: the logits hidden [T, H] x weight[V, H]^T (bf16,
+ * row-major, 16-byte aligned, H a multiple of 32) rounded to bf16 and
+ * reduced without being written: ids_out [T, k] int64 in descending order of
+ * value, equal values by ascending id (ids_out[t][0] is the argmax with
+ * torch's first-maximum rule); vals_out [T, k] fp32 (may be NULL) holds the
+ * bf16 logits, or with log_softmax != 0 their log-softmax x - logsumexp(x)
+ * over the whole row.  1 <= k <= 8, T <= 65535.  Hidden rows are taken 64
+ * at a time and the weight is streamed once per 64 rows: meant for up to 64
+ * rows (one pass over the weight), correct for any T.
+ *
+ * Replaces lm_head(h) followed by logits.argmax(-1) / logits.topk(k) in
+ * Runner._run, serving/backend.py:84-93, and the draft's argmax and
+ * torch.topk(log_softmax(logits), k), single/eval_sync.py:713-717 and
+ * :763-768; the [T, V] logits are never materialised.
+ */
+int d3d_lmhead_topk(const void* hidden, const void* weight, int T, int H, int64_t V, int k,
+                    int log_softmax, int64_t* ids_out, float* vals_out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace d3d_sample_rows needs. */
 size_t d3d_sample_workspace_bytes(int N, int64_t V);
 
