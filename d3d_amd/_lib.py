@@ -62,6 +62,7 @@ SIGNATURES = {
     "d3d_select_transfer": (_I, [_P, _I64, _I, _P, _P, _P, _I, _I, _P]),
     "d3d_topk_workspace_bytes": (_SZ, [_I, _I64, _I]),
     "d3d_topk_rows": (_I, [_P, _I, _I, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
+    "d3d_block_inputs": (_I, [_P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "d3d_lmhead_workspace_bytes": (_SZ, [_I, _I64, _I]),
     "d3d_lmhead_topk": (_I, [_P, _P, _I, _I, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
     "d3d_sample_workspace_bytes": (_SZ, [_I, _I64]),

@@ -81,6 +81,61 @@ class PagePool:
         self.free.extend(pages)
 
 
+class DevicePageTables:
+    """Device mirror of the sequences' page lists (serving/backend.py:55-76).
+
+    A [rows, num_pages] int32 pool on the device holds one row of page ids
+    per (sequence, model) table; only the ids appended since the last sync
+    cross to the device (a pinned copy), and ``block_inputs`` reads the
+    per-step tables, slots, positions and context lengths out of the pool
+    with one kernel (``d3d_block_inputs``) instead of rebuilding them from
+    host lists.  Rows freed by ``release`` are reused.
+    """
+
+    def __init__(self, num_pages: int, device, rows: int = 64):
+        self.width = num_pages
+        self.device = torch.device(device)
+        # -1 marks entries past a sequence's page list.
+        self.pool = torch.full((rows, num_pages), -1, dtype=torch.int32, device=self.device)
+        self.free_rows: List[int] = list(range(rows))
+
+    def row(self, seq: "Sequence", name: str) -> int:
+        """The pool row of seq's table ``name``, assigned on first use."""
+        row = seq.rows.get(name)
+        if row is None:
+            if not self.free_rows:
+                old = self.pool
+                self.pool = torch.full((2 * old.shape[0], self.width), -1, dtype=torch.int32, device=self.device)
+                self.pool[: old.shape[0]].copy_(old)
+                self.free_rows = list(range(old.shape[0], 2 * old.shape[0]))
+            row = self.free_rows.pop(0)
+            seq.rows[name] = row
+            seq.synced[name] = [0, 0]
+        return row
+
+    def sync(self, seq: "Sequence", name: str) -> None:
+        """Copy the page ids appended since the last sync; mark the ids a trim removed -1."""
+        row = self.row(seq, name)
+        pages = seq.pages.get(name, [])
+        state = seq.synced[name]  # [entries equal to the host list, entries written]
+        valid, written = state
+        if len(pages) > valid:
+            new = torch.empty(len(pages) - valid, dtype=torch.int32, pin_memory=True)
+            new.copy_(torch.tensor(pages[valid:], dtype=torch.int32))
+            self.pool[row, valid:len(pages)].copy_(new, non_blocking=True)
+        if written > len(pages):
+            self.pool[row, len(pages):written].fill_(-1)
+        state[0] = state[1] = len(pages)
+
+    def drop(self, seq: "Sequence", name: str) -> None:
+        row = seq.rows.pop(name, None)
+        if row is not None:
+            written = seq.synced.pop(name, [0, 0])[1]
+            if written:
+                self.pool[row, :written].fill_(-1)
+            self.free_rows.append(row)
+
+
 class PagedKV:
     """Per-layer K/V caches [num_pages, page_size, Hkv, D] bf16 (serving/backend.py:46-48)."""
 
@@ -91,6 +146,7 @@ class PagedKV:
                               device=device) for _ in range(shape.layers)]
         self.v = [torch.zeros_like(t) for t in self.k]
         self.pool = PagePool(num_pages)
+        self.tables = DevicePageTables(num_pages, device)
 
 
 class Qwen3PagedModel(torch.nn.Module):
@@ -171,6 +227,8 @@ class Sequence:
         self.token_ids = list(token_ids)
         self.prefix = len(token_ids)
         self.pages: dict = {}  # model name -> list of page ids
+        self.rows: dict = {}    # model name -> row of its device page-table pool
+        self.synced: dict = {}  # model name -> [ids equal on the device, ids written there]
 
 
 def reserve(kv: PagedKV, seq: Sequence, name: str, length: int) -> None:
@@ -186,9 +244,12 @@ def trim(kv: PagedKV, seq: Sequence, name: str, length: int) -> None:
     if len(table) > keep:
         kv.pool.release(table[keep:])
         del table[keep:]
+        if name in seq.synced:  # the device row holds the trimmed ids past keep
+            seq.synced[name][0] = min(seq.synced[name][0], keep)
 
 
 def release(kv: PagedKV, seq: Sequence, name: str) -> None:
+    kv.tables.drop(seq, name)
     kv.pool.release(seq.pages.pop(name, []))
 
 
@@ -197,20 +258,33 @@ def block_inputs(kv: PagedKV, seqs: List[Sequence], name: str, starts: List[int]
     """Page tables, slots and context lengths for a block of Q tokens at starts[b].
 
     ``width`` fixes the page-table width (and so the attention's context
-    bound, width * page_size); by default it is the longest table.
+    bound, width * page_size); by default it is the longest table.  The
+    tables come from the device mirror: per step only the request rows and
+    starts cross to the device, and one kernel gathers the tables and
+    computes the slot mapping (serving/backend.py:73-76, :123-124).
     """
     width = max(len(s.pages[name]) for s in seqs) if width is None else width
     if any(len(s.pages[name]) > width for s in seqs):
         raise ValueError("a page table is wider than the fixed width")
-    tables = torch.tensor([s.pages[name] + [0] * (width - len(s.pages[name])) for s in seqs],
-                          dtype=torch.int32)
-    st = torch.tensor(starts, dtype=torch.int64)
-    logical = st[:, None] + torch.arange(Q)[None, :]
-    slots = tables.long().gather(1, logical // kv.page_size) * kv.page_size + logical % kv.page_size
-    lens = (st + Q).to(torch.int32)
-    max_ctx = width * kv.page_size if width is not None else int(max(starts)) + Q
-    return (tables.to(device, non_blocking=True), slots.reshape(-1).to(device, non_blocking=True),
-            lens.to(device, non_blocking=True), logical.to(device, non_blocking=True), max_ctx)
+    from . import _lib
+    dev = torch.device(device)
+    T = kv.tables
+    B = len(seqs)
+    host = torch.empty(2, B, dtype=torch.int32, pin_memory=True)
+    for b, s in enumerate(seqs):
+        T.sync(s, name)
+        host[0, b] = T.row(s, name)
+        host[1, b] = int(starts[b])
+    ri = host.to(dev, non_blocking=True)
+    tables = torch.empty(B, width, dtype=torch.int32, device=dev)
+    slots = torch.empty(B * Q, dtype=torch.int64, device=dev)
+    logical = torch.empty(B, Q, dtype=torch.int64, device=dev)
+    lens = torch.empty(B, dtype=torch.int32, device=dev)
+    st = _lib.load().d3d_block_inputs(T.pool.data_ptr(), T.pool.shape[0], T.width, ri[0].data_ptr(),
+                                      ri[1].data_ptr(), B, int(Q), int(width), kv.page_size, tables.data_ptr(),
+                                      slots.data_ptr(), logical.data_ptr(), lens.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_block_inputs")
+    return tables, slots, lens, logical, width * kv.page_size
 
 
 _WARMUP: dict = {}

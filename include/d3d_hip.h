@@ -257,6 +257,25 @@ int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, int k, int lo
                   int64_t* ids_out, float* vals_out, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/*
+ * Block inputs of B requests from a device-resident page-table pool
+ * page_pool [pool_rows, pool_width] int32 (one row of page ids per sequence,
+ * -1 past its page list; rows[b] the row of request b): tables_out [B, width]
+ * int32 (the row's first width entries with -1 shown as 0, 0 past the pool
+ * width or for a row outside the pool), slots_out [B, Q] int64 = page *
+ * page_size + pos % page_size with page = row[pos / page_size] for pos =
+ * starts[b] + i (-1 when that page index is past width or the entry is -1:
+ * d3d_kv_append skips the token),
+ * positions_out [B, Q] int64 = pos and context_lens_out [B] int32 =
+ * starts[b] + Q (either may be NULL).  All pointers are device memory.
+ *
+ * Replaces the per-step host list work of Runner._tables and the slot
+ * mapping of Runner.forward, serving/backend.py:73-76 and :123-124.
+ */
+int d3d_block_inputs(const int32_t* page_pool, int pool_rows, int pool_width, const int32_t* rows,
+                     const int32_t* starts, int B, int Q, int width, int page_size, int32_t* tables_out,
+                     int64_t* slots_out, int64_t* positions_out, int32_t* context_lens_out, void* stream);
+
 /* Bytes of workspace d3d_lmhead_topk needs. */
 size_t d3d_lmhead_workspace_bytes(int T, int64_t V, int k);
 
