@@ -19,7 +19,9 @@
 //
 // The phases replace per-workgroup completion counters: on MI355X a
 // device-scope release per workgroup (L2 write-back across XCDs) and
-// same-address atomics serialise, and cost far more than two extra launches.
+// same-address atomics serialise, and cost far more than two extra launches
+// (folding phase 3 into phase 2 with a last-workgroup counter measured
+// 17 -> 22 us at one request and 43 -> 60 us at eight).
 //
 // Reference semantics (D3D repository):
 //   single/eval_sync.py:287-305           temperature softmax / greedy one-hot
