@@ -29,7 +29,7 @@
 // counts, so the grid's tail holds only empty items and short requests leave
 // no idle workgroups in the middle of the launch.
 // The G = Hq/Hkv query heads of the group times QT queries of the block
-// form the MFMA rows (row r = g*QT + qi, 16 rows per wave, at most 128).
+// form the MFMA rows (row r = g*QT + qi, 16 rows per wave, at most 16 x kMaxWaves).
 // Key t is visible to a row iff t < A or S_lo <= t < S_hi (two ranges):
 // causal A = ctx - Q + qi + 1; bidirectional A = ctx; packed A = prefix +
 // vis[qi][0], [S_lo, S_hi) = prefix + [vis[qi][1], vis[qi][2]).  Each workgroup walks its split of the
@@ -62,7 +62,14 @@ constexpr int LDS_V = TILE * ROWB;   // V region offset
 #ifndef D3D_ATTN_DEPTH
 #define D3D_ATTN_DEPTH 1
 #endif
-constexpr int kMaxWaves = 8;   // up to 128 MFMA rows per workgroup
+// Up to 16 * kMaxWaves MFMA rows per workgroup.  Four waves (64 rows) run
+// three workgroups per CU; eight-wave workgroups (128 rows) fit only one per
+// CU at this register count and measured slower on the packed draft block
+// (end-to-end 66.5 -> 68.9 steps/s with four).
+#ifndef D3D_ATTN_MAX_WAVES
+#define D3D_ATTN_MAX_WAVES 4
+#endif
+constexpr int kMaxWaves = D3D_ATTN_MAX_WAVES;
 constexpr int kMaxSplitPages = 1024;  // page ids staged per split
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
