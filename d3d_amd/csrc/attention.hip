@@ -671,7 +671,13 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
     // while each split's fp16 partial stays small against its K/V bytes.
     const int64_t units = (int64_t)B * p.nqt * Hkv;
     int64_t tps = (units * tiles + kTargetItems - 1) / kTargetItems;
-    tps = tps < 1 ? 1 : (tps > tiles ? tiles : tps);
+    // Four-wave workgroups take at least two tiles per split: at batch 1
+    // (2064 keys) that halves the fp16 partials and measured 14.9 -> 14.0 us;
+    // two-wave workgroups (the 32-row draft block) keep one-tile splits,
+    // which measured faster there.
+    const int min_tps = p.waves >= 4 ? 2 : 1;
+    tps = tps < min_tps ? min_tps : tps;
+    tps = tps > tiles ? tiles : tps;
     int tiles_per_split = (int)tps;
     if ((tiles + tiles_per_split - 1) / tiles_per_split > kMaxSplits) tiles_per_split = (tiles + kMaxSplits - 1) / kMaxSplits;
     // Split starts must be page aligned and a split's pages must fit in LDS.
