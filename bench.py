@@ -37,7 +37,7 @@ HBM_PEAK_GBPS = 8000.0
 # same process: FETCH_SIZE x 1.99920, WRITE_SIZE x 1.0.  They are measured
 # figures, not computed here; a kernel change needs a new counter pass.
 TRAFFIC_ACCEPT_B1 = 20_635_812      # stats + decide + resample, 1.095 x algorithmic
-TRAFFIC_VERIFY_ATTN_B1 = 18_057_152  # split + combine, 2.07 x algorithmic (fp16 partials)
+TRAFFIC_VERIFY_ATTN_B1 = 13_667_615  # split + combine, 1.57 x algorithmic (fp16 partials)
 
 
 def _parse():
