@@ -650,10 +650,14 @@ struct Plan {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Two workgroups are resident per CU (register-limited) on 256 CUs: 512 at
-// a time; about four rounds of work items keep the last round short.
+// Work items if every request were max_context long: about one round of the
+// 768 resident four-wave workgroups (three per CU).  Mixed lengths fill less:
+// at batch 8 (contexts 873..6219) 768 gives 448 items of 9 tiles and measured
+// 37.8 -> 35.2 us against 2048 (992 items of 4 tiles; half the fp16 partials
+// and none of the second round's idle slots); batch 1 and the draft block
+// keep their plans (the two-tile minimum and one-tile splits bind).
 #ifndef D3D_ATTN_TARGET_ITEMS
-#define D3D_ATTN_TARGET_ITEMS 2048
+#define D3D_ATTN_TARGET_ITEMS 768
 #endif
 constexpr int kTargetItems = D3D_ATTN_TARGET_ITEMS;
 
@@ -666,9 +670,7 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
     p.waves = M <= 32 ? 2 : (M <= 64 ? 4 : 8);
     const int tiles = (max_context + TILE - 1) / TILE;
     // Tiles per split: about kTargetItems (request, split, kv head, query
-    // tile) items if every request were max_context long -- several
-    // rounds of the resident workgroups, so that the last round is short,
-    // while each split's fp16 partial stays small against its K/V bytes.
+    // tile) items if every request were max_context long.
     const int64_t units = (int64_t)B * p.nqt * Hkv;
     int64_t tps = (units * tiles + kTargetItems - 1) / kTargetItems;
     // Four-wave workgroups take at least two tiles per split: at batch 1

@@ -84,6 +84,30 @@ def test_shapes_and_edges(lens, Q, Hq, Hkv, ps, causal):
     _check(out, ref)
 
 
+_RNG = np.random.default_rng(31)
+
+
+# Split layouts at their edges: one long request (many splits), 32 requests
+# with 4 query tiles each, 64 requests on 1-token pages (non-uniform page
+# fetch, one page id per key), 24-token pages (1536-key split alignment) and
+# more than 64 requests (fixed per-request split slots).
+@pytest.mark.parametrize(
+    "lens,Q,Hq,Hkv,ps",
+    [
+        ([20016], 16, 32, 8, 16),
+        (list(_RNG.integers(1, 601, 32)), 64, 32, 8, 16),
+        (list(_RNG.integers(2950, 3101, 64)), 1, 4, 1, 1),
+        ([5016, 7016, 116], 16, 32, 8, 24),
+        (list(_RNG.integers(1, 201, 70)), 1, 8, 1, 16),
+    ],
+    ids=["long-b1", "b32-four-query-tiles", "b64-one-token-pages", "pages-24", "b70"],
+)
+def test_split_layout_edges(lens, Q, Hq, Hkv, ps):
+    lens = [int(x) for x in lens]
+    out, ref = _run(lens, Q, Hq, Hkv, ps, True, seed=len(lens) + ps)
+    _check(out, ref)
+
+
 def test_tight_max_seqlen_k_matches_default_bound():
     lens = [700, 1300]
     a, ref = _run(lens, 16, 32, 8, 16, True, seed=9)
