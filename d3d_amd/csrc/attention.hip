@@ -36,10 +36,12 @@
 // context in 64-token tiles staged in LDS; all waves share a tile.  Scores
 // are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16: the
 // result layout (lane l holds tokens 4*(l/16)+r of row l%16) is, two 16-token
-// sub-tiles at a time, the A-operand layout the PV product needs, so
-// probabilities never leave registers.  V is read 4 columns at a time (one
-// 8-byte LDS read serves four 16-column output tiles), which permutes output
-// columns: tile (h, q) holds column 64h + 4j + q in lane column j.  Online softmax runs in the log2
+// sub-tiles at a time, the operand layout of P^T in O^T = V^T P^T, so
+// probabilities never leave registers, and the O^T accumulators keep each
+// lane on the query row whose softmax statistics it holds (rescaling and
+// normalising need no cross-lane moves).  V is read 4 columns at a time (one
+// 8-byte LDS read serves four 16-dim output tiles): tile (h, q) holds dim
+// 64h + 4j + q in accumulator row j.  Online softmax runs in the log2
 // domain.  With more than one split, (m, l, O) partials go to the workspace
 // and a combine kernel merges them.
 #include "d3d_common.hpp"
@@ -137,6 +139,28 @@ __device__ __forceinline__ void item_of(const Params& P, int item, int& b, int& 
     }
 }
 
+// Butterfly steps across lane groups with gfx950's permlane swaps (VALU,
+// no LDS round trip).  permlane16_swap(v, v) returns rows {0,0,2,2} and
+// {1,1,3,3} of v, permlane32_swap(v, v) halves {lo,lo} and {hi,hi}: the max
+// (or sum) of the pair is the xor-16 (xor-32) reduction step, and each lane
+// adds its own value and its partner's, which commute exactly.
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -214,6 +238,27 @@ __device__ __forceinline__ void fetch_tile_u(const Params& P, int t0, int t_begi
         reg[pss] = *reinterpret_cast<const u32x4*>(kb + lane_off);
         reg[NPASS + pss] = *reinterpret_cast<const u32x4*>(vb + lane_off);
         okmask |= (int)(pok && tw + rl < t_end) << pss;
+    }
+}
+
+// fetch_tile_u for a whole tile inside the split on in-pool pages: no
+// per-pass branches, so a two-deep prefetch loop keeps its loads in flight
+// across the compute of the tile before.
+template <int NT>
+__device__ __forceinline__ void fetch_tile_clean(const Params& P, int t0, int t_begin, const int* pages,
+                                                 uint32_t lane_off, u32x4 (&reg)[2 * TILE * 16 / NT]) {
+    constexpr int NPASS = TILE * 16 / NT;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const size_t row_bytes = (size_t)P.Hkv * D * 2;
+#pragma unroll
+    for (int pss = 0; pss < NPASS; ++pss) {
+        const int tw = t0 + 4 * w + pss * (NT / 16);
+        const int page = __builtin_amdgcn_readfirstlane(pages[(tw - t_begin) >> P.page_shift]);
+        const int base = page * P.page_size + (tw & (P.page_size - 1));
+        const char* kb = reinterpret_cast<const char*>(P.k_cache) + (size_t)base * row_bytes;
+        const char* vb = reinterpret_cast<const char*>(P.v_cache) + (size_t)base * row_bytes;
+        reg[pss] = *reinterpret_cast<const u32x4*>(kb + lane_off);
+        reg[NPASS + pss] = *reinterpret_cast<const u32x4*>(vb + lane_off);
     }
 }
 
@@ -365,9 +410,6 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         else
             fetch_tile<NT>(P, kvh, t0, t_begin, t_end, pages, (size_t)safe_row, reg, ok);
     };
-    auto store = [&](int t0, const u32x4 (&reg)[2 * TILE * 16 / NT], int ok) {
-        store_tile<NT>(lds, reg, ok, pages_ok && t0 + TILE <= t_end);
-    };
 
 
     // Q^T operand of v_mfma_f32_16x16x32_bf16: lane l holds row l%16, head
@@ -432,8 +474,7 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         for (int m = 0; m < TILE / 16; ++m)
 #pragma unroll
             for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[m][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = xor32_max(xor16_max(tmax));
         // Rescale only when the running max of some row grows (log2 domain:
         // scale * max raw score; the scale is positive, so the max commutes).
         const float m_new = fmaxf(m_run, tmax * P.scale_log2);
@@ -441,12 +482,9 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         if (__any(grow)) {
             const float alpha = grow ? (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new)) : 1.f;
             l_run *= alpha;
+            // O^T accumulators: every entry of this lane belongs to row c16.
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float a = __shfl(alpha, 4 * g4 + r, 64);
-#pragma unroll
-                for (int n = 0; n < D / 16; ++n) o[n][r] *= a;
-            }
+            for (int n = 0; n < D / 16; ++n) o[n] *= alpha;
             m_run = m_new;
         }
         // P as the A operand of 16x16x32: sub-tiles 2mp and 2mp+1 give the
@@ -490,7 +528,11 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
                                       __builtin_amdgcn_perm(vr[3][word], vr[2][word], sel),
                                       __builtin_amdgcn_perm(vr[5][word], vr[4][word], sel),
                                       __builtin_amdgcn_perm(vr[7][word], vr[6][word], sel)};
-                    o[4 * h + qq] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pop, __builtin_bit_cast(bf16x8, vw),
+                    // O^T = V^T P^T: the same registers with the operands
+                    // swapped (A = V^T, lane l row dim 64h + 4(l%16) + qq;
+                    // B = P^T, lane l column = query row l%16), so the
+                    // accumulator rows are dims and its columns query rows.
+                    o[4 * h + qq] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pop,
                                                                           o[4 * h + qq], 0, 0, 0);
                 }
             }
@@ -498,9 +540,11 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     };
 
     // Tiles are staged global -> registers -> LDS; DEPTH register sets keep
-    // that many tiles in flight while the current one is computed (one set
-    // measured faster than two: the second set's 64 VGPRs cost a wave per
-    // SIMD).
+    // that many tiles in flight while the current one is computed.  One set
+    // is the default: two (218 VGPRs, two waves per SIMD, loads verified in
+    // flight across the compute) measured batch-8 verify 35.4 -> 35.0 us and
+    // nothing at batch 1 or in the end-to-end loop, so the tile loop is not
+    // bound by load latency.
     constexpr int DEPTH = NW == 4 ? D3D_ATTN_DEPTH : 1;
     u32x4 regA[2 * TILE * 16 / NT];
     int okA = 0;
@@ -529,64 +573,76 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             compute(t0);
         }
     } else {
+        // Two register sets: A holds tile t0 and B tile t0 + TILE while both
+        // are whole and on in-pool pages, each refilled two tiles ahead with
+        // the branch-free fetch; the rest of the split (at most one whole
+        // tile and the partial one) runs the one-deep loop.
         u32x4 regB[2 * TILE * 16 / NT];
-        int okB = 0;
-        if (t_begin + TILE < t_end)
-            fetch(t_begin + TILE, regB, okB);
-        for (int t0 = t_begin; t0 < t_end; t0 += 2 * TILE) {
-            __syncthreads();
-            store(t0, regA, okA);
-            __syncthreads();
-            if (t0 + 2 * TILE < t_end) fetch(t0 + 2 * TILE, regA, okA);
-            compute(t0);
-            if (t0 + TILE < t_end) {
+        int t0 = t_begin;
+        bool a_ready = t_begin < t_end;  // regA holds tile t0
+        if (UPG && pages_ok && t0 + 2 * TILE <= t_end) {
+            // Refills are unconditional (clamped to the last whole tile):
+            // a conditional one makes the compiler drain every load before
+            // the next store.  At most two clamped refills per split are
+            // redundant, and their tile was just read.
+            const int t_lastw = t_begin + ((t_end - t_begin) / TILE - 1) * TILE;
+            fetch_tile_clean<NT>(P, t0 + TILE, t_begin, pages, lane_off, regB);
+            for (; t0 + 2 * TILE <= t_end; t0 += 2 * TILE) {
                 __syncthreads();
-                store(t0 + TILE, regB, okB);
+                store_tile<NT>(lds, regA, 0, true);
                 __syncthreads();
-                if (t0 + 3 * TILE < t_end) fetch(t0 + 3 * TILE, regB, okB);
+                a_ready = t0 + 3 * TILE <= t_end;
+                fetch_tile_clean<NT>(P, min(t0 + 2 * TILE, t_lastw), t_begin, pages, lane_off, regA);
+                compute(t0);
+                __syncthreads();
+                store_tile<NT>(lds, regB, 0, true);
+                __syncthreads();
+                fetch_tile_clean<NT>(P, min(t0 + 3 * TILE, t_lastw), t_begin, pages, lane_off, regB);
                 compute(t0 + TILE);
             }
+        }
+        if (t0 < t_end && !a_ready) fetch(t0, regA, okA);
+        for (; t0 < t_end; t0 += TILE) {
+            __syncthreads();
+            store_tile<NT>(lds, regA, okA, pages_ok && t0 + TILE <= t_end);
+            __syncthreads();
+            if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
+            compute(t0);
         }
     }
 
     // Row sums: reduce the per-lane partials over the 4 lanes of a row.
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = xor32_sum(xor16_sum(l_run));
 
+    // Lane (g4, c16) holds row c16 at dims 64h + 16 g4 + 4r + qq in
+    // o[4h + qq][r]: four consecutive dims per (h, r).
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
     if (nsplit == 1) {
+        if (row_ok) {
+            uint16_t* dst = P.out + (((size_t)b * P.Q + qi) * P.Hq + head) * D + 16 * g4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int orow = w * 16 + 4 * g4 + r;
-            const float sc_r = __shfl(inv, 4 * g4 + r, 64);
-            const int oh = kvh * P.G + orow / P.QT, oq = q0 + orow % P.QT;
-            if (orow < P.M && oq < P.Q) {
-                uint16_t* dst = P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D;
+            for (int h = 0; h < D / 64; ++h)
 #pragma unroll
-                for (int h = 0; h < D / 64; ++h) {
-                    const u32x2 v = {pack_bf16x2(o[4 * h + 0][r] * sc_r, o[4 * h + 1][r] * sc_r),
-                                     pack_bf16x2(o[4 * h + 2][r] * sc_r, o[4 * h + 3][r] * sc_r)};
-                    *reinterpret_cast<u32x2*>(dst + 64 * h + 4 * c16) = v;
+                for (int r = 0; r < 4; ++r) {
+                    const u32x2 v = {pack_bf16x2(o[4 * h + 0][r] * inv, o[4 * h + 1][r] * inv),
+                                     pack_bf16x2(o[4 * h + 2][r] * inv, o[4 * h + 3][r] * inv)};
+                    *reinterpret_cast<u32x2*>(dst + 64 * h + 4 * r) = v;
                 }
-            }
         }
     } else {
         // Normalised partial O / l in fp16 (|O / l| <= max |v|), (m, l) in fp32.
         const size_t unit = (((size_t)b * P.nqt + qt) * P.Hkv + kvh) * P.num_splits + s;
         _Float16* po = P.part_o + unit * P.M * D;
         float* pml = P.part_ml + unit * P.M * 2;
+        if (row < P.M) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int orow = w * 16 + 4 * g4 + r;
-            const float sc_r = __shfl(inv, 4 * g4 + r, 64);
-            if (orow < P.M) {
+            for (int h = 0; h < D / 64; ++h)
 #pragma unroll
-                for (int h = 0; h < D / 64; ++h) {
-                    const h16x4 v = {(_Float16)(o[4 * h + 0][r] * sc_r), (_Float16)(o[4 * h + 1][r] * sc_r),
-                                     (_Float16)(o[4 * h + 2][r] * sc_r), (_Float16)(o[4 * h + 3][r] * sc_r)};
-                    *reinterpret_cast<h16x4*>(po + (size_t)orow * D + 64 * h + 4 * c16) = v;
+                for (int r = 0; r < 4; ++r) {
+                    const h16x4 v = {(_Float16)(o[4 * h + 0][r] * inv), (_Float16)(o[4 * h + 1][r] * inv),
+                                     (_Float16)(o[4 * h + 2][r] * inv), (_Float16)(o[4 * h + 3][r] * inv)};
+                    *reinterpret_cast<h16x4*>(po + (size_t)row * D + 64 * h + 16 * g4 + 4 * r) = v;
                 }
-            }
         }
         if (g4 == 0 && row_ok) {
             pml[row * 2 + 0] = m_run;
