@@ -186,6 +186,21 @@ __device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, fl
                        lds);
 }
 
+// One descending butterfly step of the residual chunk sums (sub-chunks
+// j < nv2): sums of r and p, last positive index of each.
+template <int O>
+__device__ __forceinline__ void res_step(float (&rs)[kMaxNv2], float (&ps)[kMaxNv2], int (&lr)[kMaxNv2],
+                                         int (&lp)[kMaxNv2], int nv2) {
+#pragma unroll
+    for (int j = 0; j < kMaxNv2; ++j) {
+        if (j >= nv2) break;
+        rs[j] += xor_desc<O>(rs[j]);
+        ps[j] += xor_desc<O>(ps[j]);
+        lr[j] = max(lr[j], xor_desc<O>(lr[j]));
+        lp[j] = max(lp[j], xor_desc<O>(lp[j]));
+    }
+}
+
 template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
 __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowStat* lds, float* sM, float* sS,
                                             int* sArg, uint64_t* s_bits, float* rf, int* ri) {
@@ -328,17 +343,12 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
             }
         }
         // One combined workgroup reduction for the nv2 sub-chunks.
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-#pragma unroll
-            for (int j = 0; j < kMaxNv2; ++j) {
-                if (j >= nv2) break;
-                rs[j] += __shfl_xor(rs[j], o, kWave);
-                ps[j] += __shfl_xor(ps[j], o, kWave);
-                lr[j] = max(lr[j], __shfl_xor(lr[j], o, kWave));
-                lp[j] = max(lp[j], __shfl_xor(lp[j], o, kWave));
-            }
-        }
+        res_step<32>(rs, ps, lr, lp, nv2);
+        res_step<16>(rs, ps, lr, lp, nv2);
+        res_step<8>(rs, ps, lr, lp, nv2);
+        res_step<4>(rs, ps, lr, lp, nv2);
+        res_step<2>(rs, ps, lr, lp, nv2);
+        res_step<1>(rs, ps, lr, lp, nv2);
         __shared__ ResStat s_red[NT / kWave][kMaxNv2];
         const int lane = tid & (kWave - 1), wv = tid / kWave;
         if (lane == 0)

@@ -32,16 +32,84 @@ __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, kWave);
 }
 
+// Butterfly partners on the VALU (gfx950), without an LDS permute: the value
+// __shfl_xor(v, D) would return, for a full, convergent wave, under the
+// stated precondition on earlier steps.
+//   D = 32, 16  v_permlane32_swap / v_permlane16_swap: swap(v, v) returns
+//               halves {lo, lo} / {hi, hi} (rows {0,0,2,2} / {1,1,3,3});
+//               the partner is the one of the pair that is not this lane's.
+//   D = 8       DPP row_ror:8 (lane i <- i + 8 mod 16).
+//   D = 2, 1    DPP quad_perm [2,3,0,1] / [1,0,3,2].
+//   Descending order (32, 16, 8, 4, 2, 1), D = 4: row_ror:4, exact because
+//               the 8-step left lanes 8 apart equal.
+//   Ascending order (1, 2, 4, 8, ...), D = 4: row_half_mirror (lane j <-
+//               7 - j in each 8-lane half), exact because quads are uniform;
+//               D = 8: row_mirror (j <- 15 - j), exact because 8-lane halves
+//               are uniform.
+template <int D>
+__device__ __forceinline__ uint32_t lane_swap32(uint32_t v) {
+    if constexpr (D == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? r[0] : r[1];
+    }
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t xor_partner_desc(uint32_t v) {
+    if constexpr (D >= 16) return lane_swap32<D>(v);
+    else if constexpr (D == 8) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xf, 0xf, false);
+    else if constexpr (D == 4) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xf, 0xf, false);
+    else if constexpr (D == 2) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false);
+    else return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false);
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t xor_partner_asc(uint32_t v) {
+    if constexpr (D >= 16) return lane_swap32<D>(v);
+    else if constexpr (D == 8) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xf, 0xf, false);
+    else if constexpr (D == 4) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xf, 0xf, false);
+    else if constexpr (D == 2) return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false);
+    else return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false);
+}
+
+template <int D>
+__device__ __forceinline__ float xor_desc(float v) {
+    return __uint_as_float(xor_partner_desc<D>(__float_as_uint(v)));
+}
+template <int D>
+__device__ __forceinline__ int xor_desc(int v) {
+    return (int)xor_partner_desc<D>((uint32_t)v);
+}
+template <int D>
+__device__ __forceinline__ float xor_asc(float v) {
+    return __uint_as_float(xor_partner_asc<D>(__float_as_uint(v)));
+}
+template <int D>
+__device__ __forceinline__ int xor_asc(int v) {
+    return (int)xor_partner_asc<D>((uint32_t)v);
+}
+
+// Full-wave reductions: the descending butterfly 32, 16, ..., 1 on the
+// VALU, bit-identical to the __shfl_xor loop with the same operation order.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, wave_shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, xor_desc<32>(v));
+    v = fmaxf(v, xor_desc<16>(v));
+    v = fmaxf(v, xor_desc<8>(v));
+    v = fmaxf(v, xor_desc<4>(v));
+    v = fmaxf(v, xor_desc<2>(v));
+    return fmaxf(v, xor_desc<1>(v));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += wave_shfl_xor(v, o);
-    return v;
+    v += xor_desc<32>(v);
+    v += xor_desc<16>(v);
+    v += xor_desc<8>(v);
+    v += xor_desc<4>(v);
+    v += xor_desc<2>(v);
+    return v + xor_desc<1>(v);
 }
 
 // (value, index) argmax with torch's tie rule: larger value wins, equal values
@@ -53,13 +121,20 @@ __device__ __forceinline__ void argmax_merge(float& v, int& i, float v2, int i2)
     }
 }
 
+template <int O>
+__device__ __forceinline__ void argmax_step_desc(float& v, int& i) {
+    const float v2 = xor_desc<O>(v);
+    const int i2 = xor_desc<O>(i);
+    argmax_merge(v, i, v2, i2);
+}
+
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float v2 = wave_shfl_xor(v, o);
-        int i2 = wave_shfl_xor(i, o);
-        argmax_merge(v, i, v2, i2);
-    }
+    argmax_step_desc<32>(v, i);
+    argmax_step_desc<16>(v, i);
+    argmax_step_desc<8>(v, i);
+    argmax_step_desc<4>(v, i);
+    argmax_step_desc<2>(v, i);
+    argmax_step_desc<1>(v, i);
 }
 
 // Workgroup reductions for blockDim.x == NT (a multiple of 64).  `scratch`

@@ -162,15 +162,30 @@ __device__ __forceinline__ float inv_sum(float S) {
 }
 
 __device__ __forceinline__ int wave_max_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = max(v, xor_desc<32>(v));
+    v = max(v, xor_desc<16>(v));
+    v = max(v, xor_desc<8>(v));
+    v = max(v, xor_desc<4>(v));
+    v = max(v, xor_desc<2>(v));
+    return max(v, xor_desc<1>(v));
 }
 
 __device__ __forceinline__ int wave_min_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = min(v, xor_desc<32>(v));
+    v = min(v, xor_desc<16>(v));
+    v = min(v, xor_desc<8>(v));
+    v = min(v, xor_desc<4>(v));
+    v = min(v, xor_desc<2>(v));
+    return min(v, xor_desc<1>(v));
+}
+
+// One ascending step (lane groups of 2 * O) of the row merge: max, argmax.
+template <int O>
+__device__ __forceinline__ void merge_step_asc(float& m, float& xm, int& am) {
+    m = fmaxf(m, xor_asc<O>(m));
+    const float x2 = xor_asc<O>(xm);
+    const int a2 = xor_asc<O>(am);
+    argmax_merge(xm, am, x2, a2);
 }
 
 __device__ __forceinline__ int block_max_int(int v, int* scratch) {
@@ -290,13 +305,10 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
                     argmax_merge(xm, am, t.xmax, t.arg);
                 }
             }
-#pragma unroll
-            for (int o = 1; o < kLanesPerRow; o <<= 1) {
-                m = fmaxf(m, __shfl_xor(m, o, kWave));
-                const float x2 = __shfl_xor(xm, o, kWave);
-                const int a2 = __shfl_xor(am, o, kWave);
-                argmax_merge(xm, am, x2, a2);
-            }
+            static_assert(kLanesPerRow == 8, "three ascending merge steps");
+            merge_step_asc<1>(m, xm, am);
+            merge_step_asc<2>(m, xm, am);
+            merge_step_asc<4>(m, xm, am);
             float s = 0.f;
             if (live && M != kGreedy) {
 #pragma unroll 4
@@ -309,8 +321,9 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
                     }
                 }
             }
-#pragma unroll
-            for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o, kWave);
+            s += xor_asc<1>(s);
+            s += xor_asc<2>(s);
+            s += xor_asc<4>(s);
             if (live && g == 0) {
                 sM[r0 + rr] = m;
                 sS[r0 + rr] = s;
