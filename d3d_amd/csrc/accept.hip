@@ -418,15 +418,7 @@ __device__ __forceinline__ void resample_body(const Params& P, int b, float* s_w
         __shared__ int s_first[NT / kWave];
         __shared__ float s_base[NT / kWave];
         const int lane = tid & (kWave - 1), wv = tid / kWave;
-        float ir = mine0.r, ip = mine0.p;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const float a = __shfl_up(ir, o, kWave), q = __shfl_up(ip, o, kWave);
-            if (lane >= o) {
-                ir += a;
-                ip += q;
-            }
-        }
+        float ir = wave_incl_scan(mine0.r, lane), ip = wave_incl_scan(mine0.p, lane);
         const int mr = wave_max_int(mine0.last_r), mp = wave_max_int(mine0.last_p);
         if (lane == kWave - 1) {
             s_tot[0][wv] = ir;

@@ -75,6 +75,51 @@ __device__ __forceinline__ uint32_t xor_partner_asc(uint32_t v) {
     else return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false);
 }
 
+// The value __shfl_up(v, O) returns to lanes l >= O (lane l - O), on the
+// VALU: DPP wave_shr:1 (lane l <- l - 1 across rows) applied O times for
+// O <= 8; for 16, rows 1 and 3 take rows 0 and 2 from v_permlane16_swap and
+// row 2 takes row 1 from v_permlane32_swap of that swap's other half; for
+// 32, v_permlane32_swap.  Lanes below O get unspecified values.
+template <int O>
+__device__ __forceinline__ uint32_t up_partner(uint32_t v) {
+    if constexpr (O <= 8) {
+#pragma unroll
+        for (int k = 0; k < O; ++k) v = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf, 0xf, false);
+        return v;
+    } else if constexpr (O == 16) {
+        const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // {0,0,2,2}, {1,1,3,3}
+        const auto r32 = __builtin_amdgcn_permlane32_swap(r16[1], r16[1], false, false);  // {1,1,1,1}, ...
+        return ((threadIdx.x & 63) >> 4) == 2 ? r32[0] : r16[0];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return r[0];
+    }
+}
+
+template <int O>
+__device__ __forceinline__ float up_f(float v) {
+    return __uint_as_float(up_partner<O>(__float_as_uint(v)));
+}
+
+// Inclusive wave scan in the Hillis-Steele order (distances 1, 2, ..., 32),
+// bit-identical to the __shfl_up loop.
+__device__ __forceinline__ float wave_incl_scan(float v, int lane) {
+    float t;
+    t = up_f<1>(v);
+    if (lane >= 1) v += t;
+    t = up_f<2>(v);
+    if (lane >= 2) v += t;
+    t = up_f<4>(v);
+    if (lane >= 4) v += t;
+    t = up_f<8>(v);
+    if (lane >= 8) v += t;
+    t = up_f<16>(v);
+    if (lane >= 16) v += t;
+    t = up_f<32>(v);
+    if (lane >= 32) v += t;
+    return v;
+}
+
 template <int D>
 __device__ __forceinline__ float xor_desc(float v) {
     return __uint_as_float(xor_partner_desc<D>(__float_as_uint(v)));

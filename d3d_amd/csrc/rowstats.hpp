@@ -337,11 +337,7 @@ __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, 
 // Inclusive scan over the workgroup in thread order (fixed order).
 __device__ __forceinline__ float block_incl_scan(float v, float* s_wave) {
     const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const float t = __shfl_up(v, o, kWave);
-        if (lane >= o) v += t;
-    }
+    v = wave_incl_scan(v, lane);
     __syncthreads();
     if (lane == kWave - 1) s_wave[wv] = v;
     __syncthreads();
