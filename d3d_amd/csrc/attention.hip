@@ -663,17 +663,20 @@ constexpr int kMaxSplits = 256;
 // issued at once, from clamped slots inside the workspace; slots at or past
 // the request's split count are then excluded by selects (their bits may be
 // stale), never by a multiply.  One round trip instead of three: batch-1
-// verify 12.55 -> 12.43 us, batch-4 draft block 13.86 -> 13.53 us.  Larger
-// batches of mixed lengths would read many stale slots (about 4 MB at the
-// batch-8 draw), so they keep the exact loop.
+// verify 12.55 -> 12.43 us, batch-4 draft block 13.86 -> 13.53 us.  NSPEC
+// (4, 8, 16 or 32, the smallest at least num_splits) bounds the partial
+// outputs each thread loads.  Larger batches of mixed lengths would read
+// many stale slots (about 4 MB at the batch-8 draw), so they keep the exact
+// loop (NSPEC = 0).
 constexpr int kSpecSplits = 32;
 constexpr int kSpecBatch = 4;
 
-template <bool SPEC>
+template <int NSPEC>
 __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y;
     const int b = blockIdx.z / P.nqt, q0 = (blockIdx.z - b * P.nqt) * P.QT;
     const size_t unit0 = ((size_t)blockIdx.z * P.Hkv + kvh) * P.num_splits;
+    constexpr bool SPEC = NSPEC > 0;
     __shared__ float wts[kRowsPerCombine][SPEC ? kSpecSplits : kMaxSplits];
     __shared__ float lsum[kRowsPerCombine][SPEC ? kSpecSplits : kMaxSplits];
     __shared__ float inv_den[kRowsPerCombine];
@@ -687,9 +690,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
         const int erow = min(r0 + er, P.M - 1);
         const int esp_c = min(esp, P.num_splits - 1);
         const float2 ml = *reinterpret_cast<const float2*>(P.part_ml + ((unit0 + esp_c) * P.M + erow) * 2);
-        h16x4 hv[kSpecSplits];
+        h16x4 hv[NSPEC > 0 ? NSPEC : 1];
 #pragma unroll
-        for (int sp = 0; sp < kSpecSplits; ++sp) {
+        for (int sp = 0; sp < NSPEC; ++sp) {
             const int spc = min(sp, P.num_splits - 1);
             hv[sp] = *reinterpret_cast<const h16x4*>(P.part_o + ((unit0 + spc) * P.M + row_c) * D + c4);
         }
@@ -719,7 +722,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
         if (row >= P.M || oq >= P.Q) return;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int sp = 0; sp < kSpecSplits; ++sp) {
+        for (int sp = 0; sp < NSPEC; ++sp) {
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             const f32x4 o = {(float)hv[sp][0], (float)hv[sp][1], (float)hv[sp][2], (float)hv[sp][3]};
             acc += wts[rr][sp] * (sp < S ? o : z);
@@ -937,10 +940,17 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     if (pl.num_splits > 1)
     {
         const dim3 cgrid((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B * pl.nqt);
-        if (pl.num_splits <= kSpecSplits && B <= kSpecBatch)
-            hipLaunchKernelGGL(attn_combine_kernel<true>, cgrid, dim3(256), 0, s, P);
+        const int ns = pl.num_splits;
+        if (B > kSpecBatch || ns > kSpecSplits)
+            hipLaunchKernelGGL(attn_combine_kernel<0>, cgrid, dim3(256), 0, s, P);
+        else if (ns <= 4)
+            hipLaunchKernelGGL(attn_combine_kernel<4>, cgrid, dim3(256), 0, s, P);
+        else if (ns <= 8)
+            hipLaunchKernelGGL(attn_combine_kernel<8>, cgrid, dim3(256), 0, s, P);
+        else if (ns <= 16)
+            hipLaunchKernelGGL(attn_combine_kernel<16>, cgrid, dim3(256), 0, s, P);
         else
-            hipLaunchKernelGGL(attn_combine_kernel<false>, cgrid, dim3(256), 0, s, P);
+            hipLaunchKernelGGL(attn_combine_kernel<32>, cgrid, dim3(256), 0, s, P);
     }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
