@@ -34,10 +34,10 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # (two passes of `bench.py --no-cpu-baseline --no-models --calibrate-copy`),
 # each counter scaled by what it reads for a plain 64 MiB device copy in the
-# same process: FETCH_SIZE x 1.99920, WRITE_SIZE x 1.0.  They are measured
+# same process: FETCH_SIZE x 1.99921, WRITE_SIZE x 1.0.  They are measured
 # figures, not computed here; a kernel change needs a new counter pass.
-TRAFFIC_ACCEPT_B1 = 20_635_812      # stats + decide + resample, 1.095 x algorithmic
-TRAFFIC_VERIFY_ATTN_B1 = 13_667_615  # split + combine, 1.57 x algorithmic (fp16 partials)
+TRAFFIC_ACCEPT_B1 = 20_677_638      # stats + decide + resample, 1.098 x algorithmic
+TRAFFIC_VERIFY_ATTN_B1 = 13_697_878  # split + combine, 1.571 x algorithmic (fp16 partials)
 
 
 def _parse():
