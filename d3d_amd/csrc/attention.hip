@@ -61,9 +61,6 @@ constexpr int TILE = 64;       // tokens per KV tile
 constexpr int ROWB = D * 2 + 16;     // K
 constexpr int ROWB_V = D * 2 + 32;   // V
 constexpr int LDS_V = TILE * ROWB;   // V region offset
-#ifndef D3D_ATTN_DEPTH
-#define D3D_ATTN_DEPTH 1
-#endif
 // Up to 16 * kMaxWaves MFMA rows per workgroup.  Four waves (64 rows) run
 // three workgroups per CU; eight-wave workgroups (128 rows) fit only one per
 // CU at this register count and measured slower on the packed draft block
@@ -241,27 +238,6 @@ __device__ __forceinline__ void fetch_tile_u(const Params& P, int t0, int t_begi
     }
 }
 
-// fetch_tile_u for a whole tile inside the split on in-pool pages: no
-// per-pass branches, so a two-deep prefetch loop keeps its loads in flight
-// across the compute of the tile before.
-template <int NT>
-__device__ __forceinline__ void fetch_tile_clean(const Params& P, int t0, int t_begin, const int* pages,
-                                                 uint32_t lane_off, u32x4 (&reg)[2 * TILE * 16 / NT]) {
-    constexpr int NPASS = TILE * 16 / NT;
-    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const size_t row_bytes = (size_t)P.Hkv * D * 2;
-#pragma unroll
-    for (int pss = 0; pss < NPASS; ++pss) {
-        const int tw = t0 + 4 * w + pss * (NT / 16);
-        const int page = __builtin_amdgcn_readfirstlane(pages[(tw - t_begin) >> P.page_shift]);
-        const int base = page * P.page_size + (tw & (P.page_size - 1));
-        const char* kb = reinterpret_cast<const char*>(P.k_cache) + (size_t)base * row_bytes;
-        const char* vb = reinterpret_cast<const char*>(P.v_cache) + (size_t)base * row_bytes;
-        reg[pss] = *reinterpret_cast<const u32x4*>(kb + lane_off);
-        reg[NPASS + pss] = *reinterpret_cast<const u32x4*>(vb + lane_off);
-    }
-}
-
 // clean: every row of the tile is live and on an in-pool page (uniform), so
 // no row needs zeroing.
 template <int NT>
@@ -288,8 +264,8 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
     }
 }
 
-// Register budget: two workgroups per CU (two waves per SIMD) so that each
-// CU keeps 2 x DEPTH tiles of K/V in flight.
+// Launch bounds ask for at least two workgroups per CU; at the register
+// counts the compiler reaches, four-wave workgroups run three per CU.
 // UPG: pages are a power of two of at least 4 tokens (wave-uniform page ids).
 template <int NW, int MODE, bool UPG>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
@@ -539,76 +515,36 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
         }
     };
 
-    // Tiles are staged global -> registers -> LDS; DEPTH register sets keep
-    // that many tiles in flight while the current one is computed.  One set
-    // is the default: two (218 VGPRs, two waves per SIMD, loads verified in
-    // flight across the compute) measured batch-8 verify 35.4 -> 35.0 us and
-    // nothing at batch 1 or in the end-to-end loop, so the tile loop is not
-    // bound by load latency.
-    constexpr int DEPTH = NW == 4 ? D3D_ATTN_DEPTH : 1;
+    // Tiles are staged global -> registers -> LDS with one register set in
+    // flight while the current tile is computed.  A second set (218 VGPRs,
+    // two waves per SIMD, loads checked in the assembly to stay outstanding
+    // across the compute) measured batch-8 verify 35.4 -> 35.0 us and nothing
+    // at batch 1 or end to end: the tile loop is bound by its dependency
+    // chain, not by load latency.
     u32x4 regA[2 * TILE * 16 / NT];
     int okA = 0;
     if (t_begin < t_end) fetch(t_begin, regA, okA);
-    if constexpr (DEPTH == 1) {
-        // Whole tiles on in-pool pages store without zeroing; the split's
-        // partial last tile (and every tile of a split that names an
-        // out-of-pool page) zeroes its dead rows.  Two loops rather than a
-        // per-tile branch: with the branch inside one loop the compiler
-        // waits for the next tile's loads before the first MFMA.
-        int t0 = t_begin;
-        if (pages_ok) {
-            for (; t0 + TILE <= t_end; t0 += TILE) {
-                __syncthreads();
-                store_tile<NT>(lds, regA, okA, true);
-                __syncthreads();
-                if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
-                compute(t0);
-            }
-        }
-        for (; t0 < t_end; t0 += TILE) {
+    // Whole tiles on in-pool pages store without zeroing; the split's
+    // partial last tile (and every tile of a split that names an
+    // out-of-pool page) zeroes its dead rows.  Two loops rather than a
+    // per-tile branch: with the branch inside one loop the compiler
+    // waits for the next tile's loads before the first MFMA.
+    int t0 = t_begin;
+    if (pages_ok) {
+        for (; t0 + TILE <= t_end; t0 += TILE) {
             __syncthreads();
-            store_tile<NT>(lds, regA, okA, false);
+            store_tile<NT>(lds, regA, okA, true);
             __syncthreads();
             if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
             compute(t0);
         }
-    } else {
-        // Two register sets: A holds tile t0 and B tile t0 + TILE while both
-        // are whole and on in-pool pages, each refilled two tiles ahead with
-        // the branch-free fetch; the rest of the split (at most one whole
-        // tile and the partial one) runs the one-deep loop.
-        u32x4 regB[2 * TILE * 16 / NT];
-        int t0 = t_begin;
-        bool a_ready = t_begin < t_end;  // regA holds tile t0
-        if (UPG && pages_ok && t0 + 2 * TILE <= t_end) {
-            // Refills are unconditional (clamped to the last whole tile):
-            // a conditional one makes the compiler drain every load before
-            // the next store.  At most two clamped refills per split are
-            // redundant, and their tile was just read.
-            const int t_lastw = t_begin + ((t_end - t_begin) / TILE - 1) * TILE;
-            fetch_tile_clean<NT>(P, t0 + TILE, t_begin, pages, lane_off, regB);
-            for (; t0 + 2 * TILE <= t_end; t0 += 2 * TILE) {
-                __syncthreads();
-                store_tile<NT>(lds, regA, 0, true);
-                __syncthreads();
-                a_ready = t0 + 3 * TILE <= t_end;
-                fetch_tile_clean<NT>(P, min(t0 + 2 * TILE, t_lastw), t_begin, pages, lane_off, regA);
-                compute(t0);
-                __syncthreads();
-                store_tile<NT>(lds, regB, 0, true);
-                __syncthreads();
-                fetch_tile_clean<NT>(P, min(t0 + 3 * TILE, t_lastw), t_begin, pages, lane_off, regB);
-                compute(t0 + TILE);
-            }
-        }
-        if (t0 < t_end && !a_ready) fetch(t0, regA, okA);
-        for (; t0 < t_end; t0 += TILE) {
-            __syncthreads();
-            store_tile<NT>(lds, regA, okA, pages_ok && t0 + TILE <= t_end);
-            __syncthreads();
-            if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
-            compute(t0);
-        }
+    }
+    for (; t0 < t_end; t0 += TILE) {
+        __syncthreads();
+        store_tile<NT>(lds, regA, okA, false);
+        __syncthreads();
+        if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
+        compute(t0);
     }
 
     // Row sums: reduce the per-lane partials over the 4 lanes of a row.
