@@ -337,6 +337,7 @@ int d3d_sample_support(const float* support_vals, const int64_t* support_ids, in
  * H <= 8192): s = x + residual in fp32, residual = bf16(s) (in place),
  * out = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight).  With x == NULL the
  * residual is only normalised (the first layer's input norm) and left as is.
+ * Every pointer must be 16-byte aligned (D3D_E_UNSUPPORTED otherwise).
  *
  * Replaces RMSDNorm.add_norm_forward / norm_forward,
  * serving/vendor/ssd/layers/layernorm.py:53-98, as called by the decoder
@@ -366,7 +367,8 @@ int d3d_qk_rope_append(const void* qkv, const int64_t* positions, const void* q_
 /*
  * out [T, M] = silu(gate) * up for gate_up [T, 2M] = [gate | up] bf16,
  * evaluated in fp32 and rounded once (SiluAndMul,
- * serving/vendor/ssd/layers/activation.py:6-14).  M a multiple of 8.
+ * serving/vendor/ssd/layers/activation.py:6-14).  M a multiple of 8;
+ * gate_up and out 16-byte aligned (D3D_E_UNSUPPORTED otherwise).
  */
 int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream);
 

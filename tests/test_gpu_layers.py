@@ -45,7 +45,7 @@ def _rms_ref(s32, w, eps):
     return n * w.float()
 
 
-@pytest.mark.parametrize("T,H", [(1, 2048), (37, 4096), (128, 2048), (5, 8192), (3, 264)])
+@pytest.mark.parametrize("T,H", [(1, 2048), (37, 4096), (128, 2048), (1088, 2048), (5, 8192), (3, 264)])
 @pytest.mark.parametrize("with_x", [False, True])
 def test_add_rmsnorm(T, H, with_x):
     g = torch.Generator().manual_seed(T * 7 + H)
@@ -71,6 +71,17 @@ def test_add_rmsnorm_zero_rows_and_bad_shapes():
     # an all-zero row normalises to zero (rsqrt(eps) * 0)
     z = torch.zeros(1, 512, dtype=BF, device=DEV)
     assert torch.count_nonzero(ly.add_rmsnorm(None, z, torch.ones(512, dtype=BF, device=DEV), 1e-6)) == 0
+
+
+def test_unaligned_rows_are_rejected():
+    """add_rmsnorm and silu_mul move 16-byte vectors: a row pointer off a
+    16-byte boundary is refused with an argument error instead of being read."""
+    buf = torch.zeros(2 * 512 + 8, dtype=BF, device=DEV)
+    r = buf[1:1 + 2 * 512].view(2, 512)  # 2-byte offset, still contiguous
+    with pytest.raises(ValueError):
+        ly.add_rmsnorm(None, r, torch.ones(512, dtype=BF, device=DEV), 1e-6)
+    with pytest.raises(ValueError):
+        ly.silu_mul(buf[1:1 + 2 * 16].view(2, 16))
 
 
 def _cos_sin(pos, inv_freq):
