@@ -71,7 +71,6 @@ constexpr int LDS_V = TILE * ROWB;   // V region offset
 constexpr int kMaxWaves = D3D_ATTN_MAX_WAVES;
 constexpr int kMaxSplitPages = 1024;  // page ids staged per split
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -165,11 +164,6 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     const f32x2 v = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-}
-
-__device__ __forceinline__ s16x4 as_s16x4(uint32_t a, uint32_t b) {
-    u32x2 v = {a, b};
-    return __builtin_bit_cast(s16x4, v);
 }
 
 // Stages tokens [t0, t0 + TILE) of one KV head into registers.  Sixteen

@@ -27,11 +27,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return (uint16_t)(u >> 16);
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
-    return __shfl_xor(v, mask, kWave);
-}
-
 // Butterfly partners on the VALU (gfx950), without an LDS permute: the value
 // __shfl_xor(v, D) would return, for a full, convergent wave, under the
 // stated precondition on earlier steps.
@@ -224,22 +219,6 @@ __device__ __forceinline__ void block_argmax(float& v, int& i, float* sv, int* s
     i = si[0];
 #pragma unroll
     for (int k = 1; k < NT / kWave; ++k) argmax_merge(v, i, sv[k], si[k]);
-}
-
-// Agent-scope release/acquire used by the "last workgroup finishes" pattern.
-// Workgroups of one launch sit on different XCDs with separate L2s, so the
-// counter increment is an acq_rel atomic at agent scope: it writes back this
-// workgroup's results before the increment and invalidates stale lines after.
-__device__ __forceinline__ unsigned atomic_inc_agent(unsigned* p) {
-    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_relaxed_agent(unsigned* p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void fence_acquire_agent() {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 }  // namespace d3d
