@@ -16,7 +16,10 @@
 // workgroup argmax over its 4096-entry chunk (each thread holds 16 entries
 // in registers and excludes the ones already taken) and writes k (value,
 // index) candidates; (2) one workgroup per row merges the chunk candidates
-// the same way.  Streaming the logits once is the HBM-bound part.
+// the same way.  Streaming the logits once is the HBM-bound part.  Four
+// chunks per workgroup (64 entries per thread) measured 166 -> 340 us at
+// 1088 bf16 rows of 151936: the per-round rescans of the registers with the
+// taken mask are VALU-bound, and fewer workgroups hide less of it.
 #include "d3d_common.hpp"
 #include "rowstats.hpp"
 #include "../../include/d3d_hip.h"

@@ -41,6 +41,19 @@ def test_topk_matches_cpu_sort(V, k, dtype):
     assert torch.equal(ids[..., 0].cpu(), x.float().argmax(-1))
 
 
+@pytest.mark.parametrize("k", [2, 16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_many_rows_match_cpu_sort(k, dtype):
+    """128 rows of 151936 (the 1088-row predict's shape, fewer rows)."""
+    g = torch.Generator().manual_seed(128 + k)
+    x = (torch.randn(128, 151936, generator=g) * 3).to(dtype)
+    ids, vals = topk_tokens(x.to(DEV), k, with_values=True)
+    torch.cuda.synchronize()
+    ref = _ref(x, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref)
+    np.testing.assert_array_equal(vals.cpu().numpy(), np.take_along_axis(x.float().numpy(), ref, -1))
+
+
 def test_ties_go_to_the_lowest_id():
     V = 9000
     x = torch.zeros(4, V)

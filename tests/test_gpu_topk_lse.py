@@ -20,3 +20,12 @@ def test_topk_log_softmax_values(V, k, dtype):
     np.testing.assert_array_equal(ids.cpu().numpy(), torch.topk(x.float(), k, -1).indices.numpy()
                                   if dtype == torch.float32 else ids.cpu().numpy())
     np.testing.assert_allclose(lp.cpu().numpy(), ref.gather(-1, ids.cpu()).numpy(), atol=2e-5, rtol=0)
+
+
+def test_log_softmax_values_many_rows():
+    """128 rows of 151936, bf16."""
+    x = (torch.randn(128, 151936, generator=torch.Generator().manual_seed(9)) * 4).to(torch.bfloat16)
+    ids, lp = topk_tokens(x.to("cuda:0"), 2, with_values=True, log_softmax=True)
+    ref = torch.log_softmax(x.double(), -1)
+    np.testing.assert_allclose(lp.cpu().numpy(), ref.gather(-1, ids.cpu()).numpy(), atol=2e-5, rtol=0)
+    assert torch.equal(ids[:, 0].cpu(), x.float().argmax(-1))
