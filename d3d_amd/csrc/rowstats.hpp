@@ -270,6 +270,58 @@ template <Mode M>
 __device__ __forceinline__ void merge_row_stats(const RowStat* stats, int rows, int C, int arg_rows, float* sM,
                                                 float* sS, int* sArg, RowStat* lds) {
     const int g = threadIdx.x % kLanesPerRow;
+    // Up to kRowsPerPass rows of up to kLanesPerRow * kDirect records: each
+    // lane loads its records straight into registers (all at once, from
+    // clamped addresses) instead of staging them in LDS, and folds them in
+    // the same order as the staged path below, so the results are the same
+    // bits.
+    constexpr int kDirect = 8;
+    if (rows <= kRowsPerPass && C <= kLanesPerRow * kDirect) {
+        const int rr = threadIdx.x / kLanesPerRow;
+        const bool live = rr < rows;
+        const int last = rows * C - 1;
+        RowStat t[kDirect];
+#pragma unroll
+        for (int j = 0; j < kDirect; ++j)
+            t[j] = stats[min(rr * C + g + j * kLanesPerRow, last)];
+        float m = -INFINITY, xm = -INFINITY;
+        int am = INT_MAX;
+#pragma unroll
+        for (int j = 0; j < kDirect; ++j) {
+            if (live && g + j * kLanesPerRow < C) {
+                m = fmaxf(m, t[j].m);
+                argmax_merge(xm, am, t[j].xmax, t[j].arg);
+            }
+        }
+        static_assert(kLanesPerRow == 8, "three ascending merge steps");
+        merge_step_asc<1>(m, xm, am);
+        merge_step_asc<2>(m, xm, am);
+        merge_step_asc<4>(m, xm, am);
+        float sum = 0.f;
+        if (M != kGreedy) {
+#pragma unroll
+            for (int j = 0; j < kDirect; ++j) {
+                if (live && g + j * kLanesPerRow < C) {
+                    if constexpr (M == kProbs) {
+                        sum += t[j].s;
+                    } else {
+                        if (t[j].m != -INFINITY) sum += t[j].s * expf(t[j].m - m);
+                    }
+                }
+            }
+        }
+        sum += xor_asc<1>(sum);
+        sum += xor_asc<2>(sum);
+        sum += xor_asc<4>(sum);
+        __syncthreads();  // earlier readers of sM / sS / sArg are done
+        if (live && g == 0) {
+            sM[rr] = m;
+            sS[rr] = sum;
+            if (rr < arg_rows) sArg[rr] = am;
+        }
+        __syncthreads();
+        return;
+    }
     const int batch_rows = min(rows, kMaxStatLds / C);  // >= 1: C <= kMaxStatLds
     for (int r0 = 0; r0 < rows; r0 += batch_rows) {
         const int nr = min(batch_rows, rows - r0);
