@@ -36,8 +36,8 @@ HBM_PEAK_GBPS = 8000.0
 # each counter scaled by what it reads for a plain 64 MiB device copy in the
 # same process: FETCH_SIZE x 1.99921, WRITE_SIZE x 1.0.  They are measured
 # figures, not computed here; a kernel change needs a new counter pass.
-TRAFFIC_ACCEPT_B1 = 20_677_638      # stats + decide + resample, 1.098 x algorithmic
-TRAFFIC_VERIFY_ATTN_B1 = 13_697_878  # split + combine, 1.571 x algorithmic (fp16 partials)
+TRAFFIC_ACCEPT_B1 = 20_703_291      # stats + decide + resample, 1.099 x algorithmic
+TRAFFIC_VERIFY_ATTN_B1 = 13_703_030  # split + combine, 1.572 x algorithmic (fp16 partials)
 
 
 def _parse():
