@@ -261,7 +261,10 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
 // Launch bounds ask for at least two workgroups per CU; at the register
 // counts the compiler reaches, four-wave workgroups run three per CU.
 // UPG: pages are a power of two of at least 4 tokens (wave-uniform page ids).
-template <int NW, int MODE, bool UPG>
+// RT: row tiles of 16 per wave.  With RT = 2 each K fragment and each
+// permuted V operand read from LDS feeds two MFMAs (blocks of more than 64
+// rows per KV head: the packed draft block).
+template <int NW, int MODE, bool UPG, int RT>
 __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
     constexpr int NT = NW * 64;
     const int kvh = blockIdx.x % P.Hkv, qt = blockIdx.y;
@@ -294,26 +297,33 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     __shared__ int pages[kMaxSplitPages];
     __shared__ int s_lim[2][NW];
 
-    // This lane's query row for the Q^T operand and the softmax statistics.
-    const int row = w * 16 + c16;
-    const int gh = row / P.QT, qi = q0 + (row - gh * P.QT);
-    const bool row_ok = row < P.M && qi < P.Q;
-    const int head = kvh * P.G + (row_ok ? gh : 0);
-    // Visible keys: t < va, or vlo <= t < vhi.
-    int va = 0, vlo = 0, vhi = 0;
-    if (row_ok) {
-        if constexpr (MODE == kCausal) {
-            va = ctx - P.Q + qi + 1;
-        } else if constexpr (MODE == kFull) {
-            va = ctx;
-        } else {
-            const int pre = ctx - P.Q;
-            va = pre + P.vis[qi * 3 + 0];
-            vlo = pre + P.vis[qi * 3 + 1];
-            vhi = pre + P.vis[qi * 3 + 2];
+    // This lane's query row in row tile rt (wave w holds rows w*16*RT ..
+    // w*16*RT + 16*RT - 1) for the Q^T operand and the softmax statistics.
+    int row[RT], qi[RT], head[RT], va[RT], vlo[RT], vhi[RT];
+    bool row_ok[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        row[rt] = (w * RT + rt) * 16 + c16;
+        const int gh = row[rt] / P.QT;
+        qi[rt] = q0 + (row[rt] - gh * P.QT);
+        row_ok[rt] = row[rt] < P.M && qi[rt] < P.Q;
+        head[rt] = kvh * P.G + (row_ok[rt] ? gh : 0);
+        // Visible keys: t < va, or vlo <= t < vhi.
+        va[rt] = vlo[rt] = vhi[rt] = 0;
+        if (row_ok[rt]) {
+            if constexpr (MODE == kCausal) {
+                va[rt] = ctx - P.Q + qi[rt] + 1;
+            } else if constexpr (MODE == kFull) {
+                va[rt] = ctx;
+            } else {
+                const int pre = ctx - P.Q;
+                va[rt] = pre + P.vis[qi[rt] * 3 + 0];
+                vlo[rt] = pre + P.vis[qi[rt] * 3 + 1];
+                vhi[rt] = pre + P.vis[qi[rt] * 3 + 2];
+            }
+            va[rt] = min(va[rt], ctx);
+            vhi[rt] = min(vhi[rt], ctx);
         }
-        va = min(va, ctx);
-        vhi = min(vhi, ctx);
     }
     // Workgroup bounds: keys below a_min are visible to every row; none at
     // or past w_end is visible to any (w_end >= 0).  Causal and bidirectional
@@ -322,7 +332,13 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     // Packed blocks reduce their descriptors over the workgroup.
     int a_min = INT_MAX, w_end = 0;
     if constexpr (MODE == kPacked) {
-        int amin = row_ok ? va : INT_MAX, wend = row_ok ? max(va, vhi) : 0;
+        int amin = INT_MAX, wend = 0;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            if (row_ok[rt]) {
+                amin = min(amin, va[rt]);
+                wend = max(wend, max(va[rt], vhi[rt]));
+            }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             amin = min(amin, __shfl_xor(amin, o, 64));
@@ -385,31 +401,43 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     // Q^T operand of v_mfma_f32_16x16x32_bf16: lane l holds row l%16, head
     // dims 32*ks + 8*(l/16) + 0..7.  K is read with the same dim assignment,
     // so the product sums over every dim whatever order the hardware uses.
-    bf16x8 qop[D / 32];
+    bf16x8 qop[RT][D / 32];
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (row_ok)
-            v = *reinterpret_cast<const u32x4*>(P.q + (((size_t)b * P.Q + qi) * P.Hq + head) * D + ks * 32 + g4 * 8);
-        qop[ks] = __builtin_bit_cast(bf16x8, v);
-    }
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (row_ok[rt])
+                v = *reinterpret_cast<const u32x4*>(P.q + (((size_t)b * P.Q + qi[rt]) * P.Hq + head[rt]) * D +
+                                                    ks * 32 + g4 * 8);
+            qop[rt][ks] = __builtin_bit_cast(bf16x8, v);
+        }
 
-    f32x4 o[D / 16];
+    f32x4 o[RT][D / 16];
+    float m_run[RT], l_run[RT];
 #pragma unroll
-    for (int n = 0; n < D / 16; ++n) o[n] = {0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int n = 0; n < D / 16; ++n) o[rt][n] = {0.f, 0.f, 0.f, 0.f};
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.f;
+    }
 
     // One 64-token tile from LDS into the running (m, l, O) of each row.
     auto compute = [&](int t0) {
         const char* kl = lds;
         const char* vl = lds + LDS_V;
-        // S^T sub-tiles: sc[m][r] = score of token t0 + 16m + 4*g4 + r for row c16.
-        float sc[TILE / 16][4];
+        // S^T sub-tiles: sc[rt][m][r] = score of token t0 + 16m + 4*g4 + r for
+        // row c16 of row tile rt.
+        float sc[RT][TILE / 16][4];
         {
-            // Four independent accumulation chains, interleaved.
-            f32x4 acc[TILE / 16];
+            // Four independent accumulation chains per row tile, interleaved;
+            // each K fragment serves every row tile.
+            f32x4 acc[RT][TILE / 16];
 #pragma unroll
-            for (int m = 0; m < TILE / 16; ++m) acc[m] = {0.f, 0.f, 0.f, 0.f};
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int m = 0; m < TILE / 16; ++m) acc[rt][m] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < D / 32; ++ks) {
                 u32x4 kf[TILE / 16];
@@ -418,76 +446,90 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
                     kf[m] = *reinterpret_cast<const u32x4*>(kl + (16 * m + c16) * ROWB + (ks * 32 + g4 * 8) * 2);
 #pragma unroll
                 for (int m = 0; m < TILE / 16; ++m)
-                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[m]), qop[ks], acc[m],
-                                                                   0, 0, 0);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[rt][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[m]),
+                                                                           qop[rt][ks], acc[rt][m], 0, 0, 0);
             }
             // Raw scores; the softmax scale is applied inside the exponent.
 #pragma unroll
-            for (int m = 0; m < TILE / 16; ++m)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sc[m][r] = acc[m][r];
+                for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sc[rt][m][r] = acc[rt][m][r];
         }
         // Masking only where the tile crosses the split end or the
         // visibility frontier of some row (a uniform test).
         if (t0 + TILE > min(t_end, a_min)) {
 #pragma unroll
-            for (int m = 0; m < TILE / 16; ++m)
+            for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = t0 + 16 * m + 4 * g4 + r;
-                    const bool vis = t < va || (MODE == kPacked && t >= vlo && t < vhi);
-                    if (!(vis && t < t_end)) sc[m][r] = -INFINITY;
-                }
+                for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = t0 + 16 * m + 4 * g4 + r;
+                        const bool vis = t < va[rt] || (MODE == kPacked && t >= vlo[rt] && t < vhi[rt]);
+                        if (!(vis && t < t_end)) sc[rt][m][r] = -INFINITY;
+                    }
         }
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int m = 0; m < TILE / 16; ++m)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[m][r]);
-        tmax = xor32_max(xor16_max(tmax));
-        // Rescale only when the running max of some row grows (log2 domain:
-        // scale * max raw score; the scale is positive, so the max commutes).
-        const float m_new = fmaxf(m_run, tmax * P.scale_log2);
-        const bool grow = m_new > m_run;
-        if (__any(grow)) {
-            const float alpha = grow ? (m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new)) : 1.f;
-            l_run *= alpha;
-            // O^T accumulators: every entry of this lane belongs to row c16.
-#pragma unroll
-            for (int n = 0; n < D / 16; ++n) o[n] *= alpha;
-            m_run = m_new;
-        }
-        // P as the A operand of 16x16x32: sub-tiles 2mp and 2mp+1 give the
+        // P as the P^T operand of 16x16x32: sub-tiles 2mp and 2mp+1 give the
         // 8 token slots (4*g4 + r, then 16 + 4*g4 + r) of row c16.
         // A row with no visible key so far has m_run = -inf and only -inf
         // scores: exp2(-inf) = 0 with the offset taken as 0.
-        uint32_t pw[TILE / 16][2];
-        float psum = 0.f;
-        const float m_off = m_run == -INFINITY ? 0.f : m_run;
+        uint32_t pw[RT][TILE / 16][2];
 #pragma unroll
-        for (int m = 0; m < TILE / 16; ++m) {
-            float p[4];
+        for (int rt = 0; rt < RT; ++rt) {
+            float tmax = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[m][r], P.scale_log2, -m_off));
-                psum += p[r];
+            for (int m = 0; m < TILE / 16; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[rt][m][r]);
+            tmax = xor32_max(xor16_max(tmax));
+            // Rescale only when the running max of some row grows (log2 domain:
+            // scale * max raw score; the scale is positive, so the max commutes).
+            const float m_new = fmaxf(m_run[rt], tmax * P.scale_log2);
+            const bool grow = m_new > m_run[rt];
+            if (__any(grow)) {
+                const float alpha =
+                    grow ? (m_run[rt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new)) : 1.f;
+                l_run[rt] *= alpha;
+                // O^T accumulators: every entry of this lane belongs to row c16.
+#pragma unroll
+                for (int n = 0; n < D / 16; ++n) o[rt][n] *= alpha;
+                m_run[rt] = m_new;
             }
-            pw[m][0] = pack_bf16x2(p[0], p[1]);
-            pw[m][1] = pack_bf16x2(p[2], p[3]);
+            float psum = 0.f;
+            const float m_off = m_run[rt] == -INFINITY ? 0.f : m_run[rt];
+#pragma unroll
+            for (int m = 0; m < TILE / 16; ++m) {
+                float pr[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[rt][m][r], P.scale_log2, -m_off));
+                    psum += pr[r];
+                }
+                pw[rt][m][0] = pack_bf16x2(pr[0], pr[1]);
+                pw[rt][m][1] = pack_bf16x2(pr[2], pr[3]);
+            }
+            l_run[rt] += psum;
         }
-        l_run += psum;
 #pragma unroll
         for (int mp = 0; mp < TILE / 32; ++mp) {
-            const u32x4 pv = {pw[2 * mp][0], pw[2 * mp][1], pw[2 * mp + 1][0], pw[2 * mp + 1][1]};
-            const bf16x8 pop = __builtin_bit_cast(bf16x8, pv);
+            bf16x8 pop[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const u32x4 pv = {pw[rt][2 * mp][0], pw[rt][2 * mp][1], pw[rt][2 * mp + 1][0], pw[rt][2 * mp + 1][1]};
+                pop[rt] = __builtin_bit_cast(bf16x8, pv);
+            }
 #pragma unroll
             for (int h = 0; h < D / 64; ++h) {
                 // V rows of the 8 token slots, 4 columns 64h + 4*c16 .. +3 each.
                 u32x2 vr[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const int t = 32 * mp + 16 * (k >> 2) + 4 * g4 + (k & 3);
-                    vr[k] = *reinterpret_cast<const u32x2*>(vl + t * ROWB_V + (64 * h + 4 * c16) * 2);
+                for (int kk = 0; kk < 8; ++kk) {
+                    const int t = 32 * mp + 16 * (kk >> 2) + 4 * g4 + (kk & 3);
+                    vr[kk] = *reinterpret_cast<const u32x2*>(vl + t * ROWB_V + (64 * h + 4 * c16) * 2);
                 }
 #pragma unroll
                 for (int qq = 0; qq < 4; ++qq) {
@@ -502,8 +544,10 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
                     // swapped (A = V^T, lane l row dim 64h + 4(l%16) + qq;
                     // B = P^T, lane l column = query row l%16), so the
                     // accumulator rows are dims and its columns query rows.
-                    o[4 * h + qq] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pop,
-                                                                          o[4 * h + qq], 0, 0, 0);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        o[rt][4 * h + qq] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, vw), pop[rt], o[rt][4 * h + qq], 0, 0, 0);
                 }
             }
         }
@@ -542,41 +586,49 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
     }
 
     // Row sums: reduce the per-lane partials over the 4 lanes of a row.
-    l_run = xor32_sum(xor16_sum(l_run));
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) l_run[rt] = xor32_sum(xor16_sum(l_run[rt]));
 
-    // Lane (g4, c16) holds row c16 at dims 64h + 16 g4 + 4r + qq in
-    // o[4h + qq][r]: four consecutive dims per (h, r).
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    // Lane (g4, c16) holds row c16 of row tile rt at dims 64h + 16 g4 + 4r +
+    // qq in o[rt][4h + qq][r]: four consecutive dims per (h, r).
     if (nsplit == 1) {
-        if (row_ok) {
-            uint16_t* dst = P.out + (((size_t)b * P.Q + qi) * P.Hq + head) * D + 16 * g4;
 #pragma unroll
-            for (int h = 0; h < D / 64; ++h)
+        for (int rt = 0; rt < RT; ++rt) {
+            const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
+            if (row_ok[rt]) {
+                uint16_t* dst = P.out + (((size_t)b * P.Q + qi[rt]) * P.Hq + head[rt]) * D + 16 * g4;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const u32x2 v = {pack_bf16x2(o[4 * h + 0][r] * inv, o[4 * h + 1][r] * inv),
-                                     pack_bf16x2(o[4 * h + 2][r] * inv, o[4 * h + 3][r] * inv)};
-                    *reinterpret_cast<u32x2*>(dst + 64 * h + 4 * r) = v;
-                }
+                for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const u32x2 v = {pack_bf16x2(o[rt][4 * h + 0][r] * inv, o[rt][4 * h + 1][r] * inv),
+                                         pack_bf16x2(o[rt][4 * h + 2][r] * inv, o[rt][4 * h + 3][r] * inv)};
+                        *reinterpret_cast<u32x2*>(dst + 64 * h + 4 * r) = v;
+                    }
+            }
         }
     } else {
         // Normalised partial O / l in fp16 (|O / l| <= max |v|), (m, l) in fp32.
         const size_t unit = (((size_t)b * P.nqt + qt) * P.Hkv + kvh) * P.num_splits + s;
         _Float16* po = P.part_o + unit * P.M * D;
         float* pml = P.part_ml + unit * P.M * 2;
-        if (row < P.M) {
 #pragma unroll
-            for (int h = 0; h < D / 64; ++h)
+        for (int rt = 0; rt < RT; ++rt) {
+            const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
+            if (row[rt] < P.M) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const h16x4 v = {(_Float16)(o[4 * h + 0][r] * inv), (_Float16)(o[4 * h + 1][r] * inv),
-                                     (_Float16)(o[4 * h + 2][r] * inv), (_Float16)(o[4 * h + 3][r] * inv)};
-                    *reinterpret_cast<h16x4*>(po + (size_t)row * D + 64 * h + 16 * g4 + 4 * r) = v;
-                }
-        }
-        if (g4 == 0 && row_ok) {
-            pml[row * 2 + 0] = m_run;
-            pml[row * 2 + 1] = l_run;
+                for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const h16x4 v = {(_Float16)(o[rt][4 * h + 0][r] * inv), (_Float16)(o[rt][4 * h + 1][r] * inv),
+                                         (_Float16)(o[rt][4 * h + 2][r] * inv), (_Float16)(o[rt][4 * h + 3][r] * inv)};
+                        *reinterpret_cast<h16x4*>(po + (size_t)row[rt] * D + 64 * h + 16 * g4 + 4 * r) = v;
+                    }
+            }
+            if (g4 == 0 && row_ok[rt]) {
+                pml[row[rt] * 2 + 0] = m_run[rt];
+                pml[row[rt] * 2 + 1] = l_run[rt];
+            }
         }
     }
 }
@@ -728,7 +780,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const uint16_t* k, const
 }
 
 struct Plan {
-    int waves, split_tokens, num_splits, QT, nqt;
+    int waves, rt, split_tokens, num_splits, QT, nqt;
     bool valid;
     size_t part_o_bytes, part_ml_bytes, total;
 };
@@ -749,15 +801,25 @@ constexpr int kTargetItems = D3D_ATTN_TARGET_ITEMS;
 static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
     Plan p;
     const int G = Hq / Hkv;
-    p.QT = Q < kMaxWaves * 16 / G ? Q : kMaxWaves * 16 / G;
+    // Blocks of more than 64 rows per KV head (G x Q) take two row tiles per
+    // wave in four-wave workgroups: 128 rows, each LDS fragment used twice.
+#ifndef D3D_ATTN_ROW_TILES
+#define D3D_ATTN_ROW_TILES 2
+#endif
+    p.rt = (kMaxWaves == 4 && G * Q > 64 && D3D_ATTN_ROW_TILES == 2) ? 2 : 1;
+    const int rows = kMaxWaves * 16 * p.rt;
+    p.QT = Q < rows / G ? Q : rows / G;
     p.nqt = (Q + p.QT - 1) / p.QT;
     const int M = G * p.QT;
-    p.waves = M <= 32 ? 2 : (M <= 64 ? 4 : 8);
+    p.waves = p.rt == 2 ? 4 : (M <= 32 ? 2 : (M <= 64 ? 4 : 8));
     const int tiles = (max_context + TILE - 1) / TILE;
     // Tiles per split: about kTargetItems (request, split, kv head, query
     // tile) items if every request were max_context long.
     const int64_t units = (int64_t)B * p.nqt * Hkv;
-    int64_t tps = (units * tiles + kTargetItems - 1) / kTargetItems;
+    // Two-row-tile workgroups (238 VGPRs) run two per CU, not three: about
+    // one round of them is 512 items.
+    const int64_t target = p.rt == 2 ? 512 : kTargetItems;
+    int64_t tps = (units * tiles + target - 1) / target;
     // Four-wave workgroups take at least two tiles per split: at batch 1
     // (2064 keys) that halves the fp16 partials and measured 14.9 -> 14.0 us;
     // two-wave workgroups (the 32-row draft block) keep one-tile splits,
@@ -850,21 +912,28 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     switch (pl.waves) {
         case 2:
             if (upg)
-                hipLaunchKernelGGL((attn_split_kernel<2, MODE, true>), grid, dim3(128), 0, s, P);
+                hipLaunchKernelGGL((attn_split_kernel<2, MODE, true, 1>), grid, dim3(128), 0, s, P);
             else
-                hipLaunchKernelGGL((attn_split_kernel<2, MODE, false>), grid, dim3(128), 0, s, P);
+                hipLaunchKernelGGL((attn_split_kernel<2, MODE, false, 1>), grid, dim3(128), 0, s, P);
             break;
         case 4:
-            if (upg)
-                hipLaunchKernelGGL((attn_split_kernel<4, MODE, true>), grid, dim3(256), 0, s, P);
-            else
-                hipLaunchKernelGGL((attn_split_kernel<4, MODE, false>), grid, dim3(256), 0, s, P);
+            if (pl.rt == 2) {
+                if (upg)
+                    hipLaunchKernelGGL((attn_split_kernel<4, MODE, true, 2>), grid, dim3(256), 0, s, P);
+                else
+                    hipLaunchKernelGGL((attn_split_kernel<4, MODE, false, 2>), grid, dim3(256), 0, s, P);
+            } else {
+                if (upg)
+                    hipLaunchKernelGGL((attn_split_kernel<4, MODE, true, 1>), grid, dim3(256), 0, s, P);
+                else
+                    hipLaunchKernelGGL((attn_split_kernel<4, MODE, false, 1>), grid, dim3(256), 0, s, P);
+            }
             break;
         default:
             if (upg)
-                hipLaunchKernelGGL((attn_split_kernel<8, MODE, true>), grid, dim3(512), 0, s, P);
+                hipLaunchKernelGGL((attn_split_kernel<8, MODE, true, 1>), grid, dim3(512), 0, s, P);
             else
-                hipLaunchKernelGGL((attn_split_kernel<8, MODE, false>), grid, dim3(512), 0, s, P);
+                hipLaunchKernelGGL((attn_split_kernel<8, MODE, false, 1>), grid, dim3(512), 0, s, P);
             break;
     }
     if (pl.num_splits > 1)
