@@ -54,29 +54,55 @@ def test_many_rows_match_cpu_sort(k, dtype):
     np.testing.assert_array_equal(vals.cpu().numpy(), np.take_along_axis(x.float().numpy(), ref, -1))
 
 
-def test_ties_go_to_the_lowest_id():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ties_go_to_the_lowest_id(dtype):
     V = 9000
     x = torch.zeros(4, V)
     x[0, [17, 4095, 4096, 8999]] = 5.0     # equal maxima across chunks
     x[1] = 1.0                              # constant row
     x[2, ::3] = 2.0
     x[3, 8000:] = -1.0
+    x = x.to(dtype)
     ids = topk_tokens(x.to(DEV), 5).cpu().numpy()
     np.testing.assert_array_equal(ids, _ref(x, 5))
     assert list(ids[0, :4]) == [17, 4095, 4096, 8999]
     assert list(ids[1]) == [0, 1, 2, 3, 4]
 
 
-def test_nan_and_infinities():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nan_and_infinities(dtype):
     V = 5000
     x = torch.randn(2, V, generator=torch.Generator().manual_seed(1))
     x[0, 10] = float("nan")
     x[0, 11] = float("inf")
     x[1, :] = float("-inf")
     x[1, 4999] = float("nan")
+    x = x.to(dtype)
     ids = topk_tokens(x.to(DEV), 3).cpu().numpy()
     assert ids[0, 0] == 11 and 10 not in ids[0]
     np.testing.assert_array_equal(ids[1], [0, 1, 2])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_signed_zeros_tie_and_keep_their_sign(dtype):
+    """-0 and +0 are equal values (ties by id); the returned values keep
+    their sign bits; -inf entries are selectable, NaN never."""
+    V = 9000
+    x = torch.full((3, V), -1.0)
+    x[0, [5, 4100, 30]] = torch.tensor([-0.0, 0.0, -0.0])
+    x[1, :] = float("-inf")
+    x[1, [7, 8001]] = float("nan")
+    x[2, :] = -0.0
+    x[2, 3] = 0.0
+    x = x.to(dtype)
+    ids, vals = topk_tokens(x.to(DEV), 4, with_values=True)
+    torch.cuda.synchronize()
+    ids, vals = ids.cpu().numpy(), vals.cpu().numpy()
+    np.testing.assert_array_equal(ids, _ref(x, 4))
+    assert list(ids[0, :3]) == [5, 30, 4100] and list(ids[1]) == [0, 1, 2, 3]
+    np.testing.assert_array_equal(np.signbit(vals[0, :3]), [True, True, False])
+    np.testing.assert_array_equal(np.signbit(vals[2]), [True, True, True, False])
+    assert list(ids[2]) == [0, 1, 2, 3]
 
 
 def test_k_equals_vocabulary():
