@@ -20,9 +20,10 @@
 // chunks per workgroup (64 entries per thread) measured 166 -> 340 us at
 // 1088 bf16 rows of 151936: the per-round rescans of the registers are
 // VALU-bound, and fewer workgroups hide less of it.  For bf16 rows each
-// entry is one sortable integer key (value, position, sign of zero), so a
-// round's rescan is 16 integer maxes: 161.8 -> 138.8 us at that shape
-// against the (value, index) compares with a taken mask that fp32 rows use.
+// entry is one sortable integer key (value, position in the chunk, sign of
+// zero), so a round is 16 integer maxes, an unsigned-max butterfly and one
+// barrier: 161.8 -> 136.3 us at that shape against the (value, index)
+// compares with a taken mask and two-barrier argmax that fp32 rows keep.
 #include "d3d_common.hpp"
 #include "rowstats.hpp"
 #include "../../include/d3d_hip.h"
@@ -35,6 +36,12 @@ namespace topk {
 using namespace rows;
 
 constexpr int kMaxK = 64;
+// bf16 rows: vocabulary chunks per workgroup (16 entries each per thread).
+// Two measured 135.6 -> 153.3 us at 1088 rows of 151936 (77 VGPRs, fewer
+// waves per SIMD, half the workgroups).
+constexpr int kBf16Chunks = 1;
+template <int DT>
+constexpr int chunks_per_wg() { return DT == kBF16 ? kBf16Chunks : 1; }
 constexpr int kMaxCand = 8192;  // chunk candidates per row merged in LDS
 
 struct Cand {
@@ -51,6 +58,22 @@ struct Params {
     float* vals;      // [N, k] (may be null)
 };
 
+// Round 0's winner is the chunk max: the chunk's share of logsumexp,
+// (max, sum exp(x - max)) over the live entries.
+template <int DT, int LT>
+__device__ __forceinline__ void chunk_lse(const Params& P, const float (&x)[LT], int first, float wv, int n, int c,
+                                          float* sv) {
+    constexpr int E = Vec<DT>::E;
+    float se = 0.f;
+    if (wv != -INFINITY) {
+#pragma unroll
+        for (int l = 0; l < LT; ++l)
+            if (tile_index<DT>(first, NT * E, l) < P.V) se += expf(x[l] - wv);
+    }
+    se = block_sum<NT>(se, sv);
+    if (threadIdx.x == 0) P.lse[(size_t)n * P.C + c] = make_float2(wv, se);
+}
+
 template <int DT, bool VEC>
 __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
     constexpr int E = Vec<DT>::E;
@@ -58,78 +81,85 @@ __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
     __shared__ float sv[NT / kWave];
     __shared__ int si[NT / kWave];
     const void* row = row_ptr<DT>(P.logits, n, P.V);
-    const int first = c * kChunk + threadIdx.x * E;
-    float x[L];
-    load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
-    // bf16 rows: entry l's key is its order-preserving 16-bit value (-0
-    // ordered as +0), then 15 - l, then a -0 flag, so one integer max per
-    // entry finds the thread's best: the larger value, and among equal
-    // values the lower index (indices rise with l; the flag never decides,
-    // as the l field differs first).  Key 0 marks NaN, entries past the row
-    // and entries already taken; -inf keeps a positive key, as its
-    // (value, index) pair is selectable.
-    static_assert(DT != kBF16 || L == 16, "four key bits for the entry");
-    uint32_t key[L];
+    constexpr int LT = L * chunks_per_wg<DT>();  // entries per thread
+    constexpr int span = kChunk * chunks_per_wg<DT>();
+    const int first = c * span + threadIdx.x * E;
+    float x[LT];
+    load_tile<DT, VEC, true, LT>(row, P.V, first, NT * E, -INFINITY, x);
     if constexpr (DT == kBF16) {
+        // Each entry is one sortable key: its order-preserving 16-bit value
+        // (-0 ordered as +0), then span - 1 - its position in the span,
+        // then a -0 flag.  Keys are unique within the chunk, and the
+        // largest is the larger value, among equal values the lower index
+        // (the flag never decides, as the positions differ first).  So a
+        // round is an unsigned max: LT per thread, a DPP butterfly per wave,
+        // one LDS slot per wave and round, one barrier.  Key 0 marks NaN,
+        // entries past the row and entries taken; -inf keeps a positive key,
+        // as its (value, index) pair is selectable.
+        constexpr int kPosBits = 13;
+        static_assert(span <= (1 << kPosBits), "position field of the key");
+        __shared__ uint32_t swin[kMaxK][NT / kWave];
+        const int base = c * span, w = threadIdx.x / kWave;
+        uint32_t key[LT];
 #pragma unroll
-        for (int l = 0; l < L; ++l) {
+        for (int l = 0; l < LT; ++l) {
+            const int e = tile_index<DT>(first, NT * E, l);
             const uint32_t u = __float_as_uint(x[l]) >> 16;
             const uint32_t nz = u == 0x8000u;
             const uint32_t v = nz ? 0u : u;
             const bool nan = (v & 0x7f80u) == 0x7f80u && (v & 0x7fu);
             const uint32_t ord = (v & 0x8000u) ? (~v & 0xffffu) : (v | 0x8000u);
-            key[l] = (nan || tile_index<DT>(first, NT * E, l) >= P.V) ? 0u
-                                                                      : (ord << 5) | ((uint32_t)(15 - l) << 1) | nz;
+            key[l] = (nan || e >= P.V) ? 0u : (ord << (kPosBits + 1)) | ((uint32_t)(span - 1 - (e - base)) << 1) | nz;
         }
+        for (int r = 0; r < P.k; ++r) {
+            uint32_t win = key[0];
+#pragma unroll
+            for (int l = 1; l < LT; ++l) win = max(win, key[l]);
+            win = max(win, xor_partner_desc<32>(win));
+            win = max(win, xor_partner_desc<16>(win));
+            win = max(win, xor_partner_desc<8>(win));
+            win = max(win, xor_partner_desc<4>(win));
+            win = max(win, xor_partner_desc<2>(win));
+            win = max(win, xor_partner_desc<1>(win));
+            if ((threadIdx.x & (kWave - 1)) == 0) swin[r][w] = win;
+            __syncthreads();
+            win = swin[r][0];
+#pragma unroll
+            for (int k = 1; k < NT / kWave; ++k) win = max(win, swin[r][k]);
+#pragma unroll
+            for (int l = 0; l < LT; ++l)
+                if (key[l] == win) key[l] = 0;  // the winner, in its owner's registers
+            float wv = -INFINITY;
+            int wi = INT_MAX;
+            if (win) {
+                const uint32_t ord = win >> (kPosBits + 1);
+                const uint32_t u = ((ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu)) | ((win & 1u) << 15);
+                wv = __uint_as_float(u << 16);
+                wi = base + span - 1 - (int)((win >> 1) & ((1u << kPosBits) - 1));
+            }
+            if (threadIdx.x == 0) P.cand[((size_t)n * P.C + c) * P.k + r] = Cand{wv, wi};
+            if (r == 0 && P.lse) chunk_lse<DT>(P, x, first, wv, n, c, sv);
+        }
+        return;
     }
-    uint32_t taken = 0;  // fp32 rows: bit l, entry l already selected
+    uint32_t taken = 0;  // bit l: entry l already selected
     for (int r = 0; r < P.k; ++r) {
         float bv = -INFINITY;
         int bi = INT_MAX;
-        uint32_t best = 0;
-        if constexpr (DT == kBF16) {
 #pragma unroll
-            for (int l = 0; l < L; ++l) best = max(best, key[l]);
-            if (best) {
-                const uint32_t ord = best >> 5;
-                const uint32_t u = ((ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu)) | ((best & 1u) << 15);
-                bv = __uint_as_float(u << 16);
-                bi = tile_index<DT>(first, NT * E, 15 - (int)((best >> 1) & 15u));
-            }
-        } else {
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const int e = tile_index<DT>(first, NT * E, l);
-                if (!((taken >> l) & 1u) && e < P.V) argmax_merge(bv, bi, x[l], e);
-            }
+        for (int l = 0; l < LT; ++l) {
+            const int e = tile_index<DT>(first, NT * E, l);
+            if (!((taken >> l) & 1u) && e < P.V) argmax_merge(bv, bi, x[l], e);
         }
         float wv = bv;
         int wi = bi;
         block_argmax<NT>(wv, wi, sv, si);
         // The owner of the winning entry excludes it from later rounds.
-        if constexpr (DT == kBF16) {
-            if (best && bi == wi) {
 #pragma unroll
-                for (int l = 0; l < L; ++l)
-                    if (key[l] == best) key[l] = 0;
-            }
-        } else {
-#pragma unroll
-            for (int l = 0; l < L; ++l)
-                if (tile_index<DT>(first, NT * E, l) == wi) taken |= 1u << l;
-        }
+        for (int l = 0; l < LT; ++l)
+            if (tile_index<DT>(first, NT * E, l) == wi) taken |= 1u << l;
         if (threadIdx.x == 0) P.cand[((size_t)n * P.C + c) * P.k + r] = Cand{wv, wi};
-        if (r == 0 && P.lse) {
-            // Round 0's winner is the chunk max: the chunk's share of logsumexp.
-            float se = 0.f;
-            if (wv != -INFINITY) {
-#pragma unroll
-                for (int l = 0; l < L; ++l)
-                    if (tile_index<DT>(first, NT * E, l) < P.V) se += expf(x[l] - wv);
-            }
-            se = block_sum<NT>(se, sv);
-            if (threadIdx.x == 0) P.lse[(size_t)n * P.C + c] = make_float2(wv, se);
-        }
+        if (r == 0 && P.lse) chunk_lse<DT>(P, x, first, wv, n, c, sv);
     }
 }
 
@@ -534,7 +564,8 @@ extern "C" int d3d_topk_rows(const void* logits, int dtype, int N, int64_t V, in
     P.logits = logits;
     P.N = N;
     P.V = (int)V;
-    P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
+    const int span = rows::kChunk * (dtype == D3D_DTYPE_BF16 ? kBf16Chunks : 1);
+    P.C = (int)((V + span - 1) / span);
     P.k = k;
     if ((int64_t)P.C * k > kMaxCand) return D3D_E_SHAPE;
     if (workspace_bytes < d3d_topk_workspace_bytes(N, V, k)) return D3D_E_WORKSPACE;
