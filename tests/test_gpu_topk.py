@@ -28,7 +28,7 @@ def _ref(x: torch.Tensor, k: int):
 
 
 @pytest.mark.parametrize("V", [151936, 4099, 4096, 100])
-@pytest.mark.parametrize("k", [1, 2, 4, 16])
+@pytest.mark.parametrize("k", [1, 2, 4, 16, 64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_topk_matches_cpu_sort(V, k, dtype):
     g = torch.Generator().manual_seed(V + k)
