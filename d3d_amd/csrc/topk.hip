@@ -142,6 +142,7 @@ __global__ __launch_bounds__(NT) void topk_chunk_kernel(Params P) {
         }
         return;
     }
+    static_assert(LT <= 32, "one mask bit per entry");
     uint32_t taken = 0;  // bit l: entry l already selected
     for (int r = 0; r < P.k; ++r) {
         float bv = -INFINITY;
