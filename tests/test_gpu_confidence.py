@@ -76,3 +76,33 @@ def test_positions_without_masks_are_untouched():
     x0, _ = draft.confidence_topk_unmask(logits.to(dev), blk, MASK, 16)
     assert torch.equal(blk.cpu(), block)
     assert torch.equal(x0.cpu(), logits.argmax(-1))
+
+
+@pytest.mark.parametrize("T", [0.0, 0.7])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_exact_ties_go_to_lower_id_and_position(T, dtype):
+    """Equal maxima in a row give the lowest id as x0; positions with equal
+    confidences are unmasked lowest position first.  Tied rows are
+    identical, so their confidences are equal bit for bit."""
+    V, Q = 4099, 16
+    g = torch.Generator().manual_seed(41)
+    logits = torch.randn(2, Q, V, generator=g)
+    peaked = torch.randn(V, generator=g)
+    peaked[[77, 5, 4098]] = 12.0
+    for p in (9, 3, 12, 7):
+        logits[0, p] = peaked
+    logits[1, :] = peaked  # every position ties
+    block = torch.full((2, Q), MASK, dtype=torch.int64)
+    dev = torch.device("cuda:0")
+    lg = logits.to(dtype)
+    blk = block.to(dev)
+    x0, conf = draft.confidence_topk_unmask(lg.to(dev), blk, MASK, 2, T)
+    torch.cuda.synchronize()
+    ref_blk, ref_x0, _ = oracle.confidence_topk(lg.float().numpy(), block.numpy(), MASK, 2, T)
+    x0, blk, conf = x0.cpu().numpy(), blk.cpu().numpy(), conf.cpu().numpy()
+    np.testing.assert_array_equal(x0, ref_x0)
+    assert all(x0[0, p] == 5 for p in (3, 7, 9, 12)) and (x0[1] == 5).all()
+    assert len({conf[0, p] for p in (3, 7, 9, 12)}) == 1 and len(set(conf[1])) == 1
+    np.testing.assert_array_equal(blk, ref_blk)
+    assert list(np.flatnonzero(blk[0] != MASK)) == [3, 7]
+    assert list(np.flatnonzero(blk[1] != MASK)) == [0, 1]
