@@ -649,11 +649,17 @@ constexpr int kMaxSplits = 256;
 // (4, 8, 16 or 32, the smallest at least num_splits) bounds the partial
 // outputs each thread loads.  Larger batches of mixed lengths would read
 // many stale slots (about 4 MB at the batch-8 draw), so they keep the exact
-// loop (NSPEC = 0).
+// loop (NSPEC = 0), or with CTX_FIRST read the request's context length
+// first and clamp every slot to its own split count: two round trips and no
+// stale slots (batch-8 draw 34.3 -> 32.8 us for the whole call, against the
+// exact loop's three round trips).
+#ifndef D3D_ATTN_CTX_FIRST_COMBINE
+#define D3D_ATTN_CTX_FIRST_COMBINE 1
+#endif
 constexpr int kSpecSplits = 32;
 constexpr int kSpecBatch = 4;
 
-template <int NSPEC>
+template <int NSPEC, bool CTX_FIRST = false>
 __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     const int r0 = blockIdx.x * kRowsPerCombine, kvh = blockIdx.y;
     const int b = blockIdx.z / P.nqt, q0 = (blockIdx.z - b * P.nqt) * P.QT;
@@ -668,18 +674,26 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     int S;
     if constexpr (SPEC) {
         static_assert(kRowsPerCombine * kSpecSplits == 256, "one statistic per thread");
+        int slots = P.num_splits;  // slots loaded are clamped below this
+        if constexpr (CTX_FIRST) {
+            S = splits_of(P, b);
+            if (S == 1) return;  // the split kernel wrote this request's output
+            slots = S;
+        }
         const int er = threadIdx.x / kSpecSplits, esp = threadIdx.x % kSpecSplits;
         const int erow = min(r0 + er, P.M - 1);
-        const int esp_c = min(esp, P.num_splits - 1);
+        const int esp_c = min(esp, slots - 1);
         const float2 ml = *reinterpret_cast<const float2*>(P.part_ml + ((unit0 + esp_c) * P.M + erow) * 2);
         h16x4 hv[NSPEC > 0 ? NSPEC : 1];
 #pragma unroll
         for (int sp = 0; sp < NSPEC; ++sp) {
-            const int spc = min(sp, P.num_splits - 1);
+            const int spc = min(sp, slots - 1);
             hv[sp] = *reinterpret_cast<const h16x4*>(P.part_o + ((unit0 + spc) * P.M + row_c) * D + c4);
         }
-        S = splits_of(P, b);
-        if (S == 1) return;  // the split kernel wrote this request's output
+        if constexpr (!CTX_FIRST) {
+            S = splits_of(P, b);
+            if (S == 1) return;  // the split kernel wrote this request's output
+        }
         const bool live = esp < S && r0 + er < P.M;
         wts[er][esp] = live ? ml.x : -INFINITY;
         lsum[er][esp] = live ? ml.y : 0.f;
@@ -761,6 +775,20 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     const float sc = inv_den[rr];
     const u32x2 v = {pack_bf16x2(acc[0] * sc, acc[1] * sc), pack_bf16x2(acc[2] * sc, acc[3] * sc)};
     *reinterpret_cast<u32x2*>(P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D + c4) = v;
+}
+
+// Combine with every load issued at once, NSPEC the smallest of 4, 8, 16, 32
+// covering ns splits.
+template <bool CTX_FIRST>
+static void launch_slot_combine(int ns, dim3 grid, hipStream_t s, const Params& P) {
+    if (ns <= 4)
+        hipLaunchKernelGGL((attn_combine_kernel<4, CTX_FIRST>), grid, dim3(256), 0, s, P);
+    else if (ns <= 8)
+        hipLaunchKernelGGL((attn_combine_kernel<8, CTX_FIRST>), grid, dim3(256), 0, s, P);
+    else if (ns <= 16)
+        hipLaunchKernelGGL((attn_combine_kernel<16, CTX_FIRST>), grid, dim3(256), 0, s, P);
+    else
+        hipLaunchKernelGGL((attn_combine_kernel<32, CTX_FIRST>), grid, dim3(256), 0, s, P);
 }
 
 // KV append: one workgroup per token, 16 bytes per thread (K then V).
@@ -940,16 +968,12 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
     {
         const dim3 cgrid((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B * pl.nqt);
         const int ns = pl.num_splits;
-        if (B > kSpecBatch || ns > kSpecSplits)
+        if (ns > kSpecSplits || (B > kSpecBatch && !D3D_ATTN_CTX_FIRST_COMBINE))
             hipLaunchKernelGGL(attn_combine_kernel<0>, cgrid, dim3(256), 0, s, P);
-        else if (ns <= 4)
-            hipLaunchKernelGGL(attn_combine_kernel<4>, cgrid, dim3(256), 0, s, P);
-        else if (ns <= 8)
-            hipLaunchKernelGGL(attn_combine_kernel<8>, cgrid, dim3(256), 0, s, P);
-        else if (ns <= 16)
-            hipLaunchKernelGGL(attn_combine_kernel<16>, cgrid, dim3(256), 0, s, P);
+        else if (B > kSpecBatch)
+            launch_slot_combine<true>(ns, cgrid, s, P);
         else
-            hipLaunchKernelGGL(attn_combine_kernel<32>, cgrid, dim3(256), 0, s, P);
+            launch_slot_combine<false>(ns, cgrid, s, P);
     }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
