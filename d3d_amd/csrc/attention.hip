@@ -646,13 +646,22 @@ constexpr int kMaxSplits = 256;
 // the request's split count are then excluded by selects (their bits may be
 // stale), never by a multiply.  One round trip instead of three: batch-1
 // verify 12.55 -> 12.43 us, batch-4 draft block 13.86 -> 13.53 us.  NSPEC
-// (4, 8, 16 or 32, the smallest at least num_splits) bounds the partial
-// outputs each thread loads.  Larger batches of mixed lengths would read
+// (4, 8, 16, 20, 24 or 32, the smallest at least num_splits) bounds the
+// partial outputs each thread loads.  The 17 splits of a 2064-key context
+// took 32 slots (118 VGPRs, each thread's loads and conversions issued in
+// one long chain) before the 20- and 24-slot forms: batch-1 verify 13.49 ->
+// 11.96 us, batch-4 draft block 13.32 -> 11.86 us.  Larger batches of mixed lengths would read
 // many stale slots (about 4 MB at the batch-8 draw), so they keep the exact
 // loop (NSPEC = 0), or with CTX_FIRST read the request's context length
 // first and clamp every slot to its own split count: two round trips and no
 // stale slots (batch-8 draw 34.3 -> 32.8 us for the whole call, against the
 // exact loop's three round trips).
+#ifndef D3D_ATTN_SLOTS20
+#define D3D_ATTN_SLOTS20 1
+#endif
+#ifndef D3D_ATTN_SLOTS24
+#define D3D_ATTN_SLOTS24 1
+#endif
 #ifndef D3D_ATTN_CTX_FIRST_COMBINE
 #define D3D_ATTN_CTX_FIRST_COMBINE 1
 #endif
@@ -777,8 +786,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     *reinterpret_cast<u32x2*>(P.out + (((size_t)b * P.Q + oq) * P.Hq + oh) * D + c4) = v;
 }
 
-// Combine with every load issued at once, NSPEC the smallest of 4, 8, 16, 32
-// covering ns splits.
+// Combine with every load issued at once, NSPEC the smallest of 4, 8, 16,
+// 20, 24, 32 covering ns splits.
 template <bool CTX_FIRST>
 static void launch_slot_combine(int ns, dim3 grid, hipStream_t s, const Params& P) {
     if (ns <= 4)
@@ -787,6 +796,10 @@ static void launch_slot_combine(int ns, dim3 grid, hipStream_t s, const Params& 
         hipLaunchKernelGGL((attn_combine_kernel<8, CTX_FIRST>), grid, dim3(256), 0, s, P);
     else if (ns <= 16)
         hipLaunchKernelGGL((attn_combine_kernel<16, CTX_FIRST>), grid, dim3(256), 0, s, P);
+    else if (ns <= 20 && D3D_ATTN_SLOTS20)
+        hipLaunchKernelGGL((attn_combine_kernel<20, CTX_FIRST>), grid, dim3(256), 0, s, P);
+    else if (ns <= 24 && D3D_ATTN_SLOTS24)
+        hipLaunchKernelGGL((attn_combine_kernel<24, CTX_FIRST>), grid, dim3(256), 0, s, P);
     else
         hipLaunchKernelGGL((attn_combine_kernel<32, CTX_FIRST>), grid, dim3(256), 0, s, P);
 }
