@@ -37,7 +37,7 @@ HBM_PEAK_GBPS = 8000.0
 # same process: FETCH_SIZE x 1.99921, WRITE_SIZE x 1.0.  They are measured
 # figures, not computed here; a kernel change needs a new counter pass.
 TRAFFIC_ACCEPT_B1 = 20_703_291      # stats + decide + resample, 1.099 x algorithmic
-TRAFFIC_VERIFY_ATTN_B1 = 13_697_896  # split + combine, 1.571 x algorithmic (fp16 partials)
+TRAFFIC_VERIFY_ATTN_B1 = 13_678_652  # split + combine, 1.569 x algorithmic (fp16 partials)
 
 
 def _parse():
