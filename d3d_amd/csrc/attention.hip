@@ -61,14 +61,12 @@ constexpr int TILE = 64;       // tokens per KV tile
 constexpr int ROWB = D * 2 + 16;     // K
 constexpr int ROWB_V = D * 2 + 32;   // V
 constexpr int LDS_V = TILE * ROWB;   // V region offset
-// Up to 16 * kMaxWaves MFMA rows per workgroup.  Four waves (64 rows) run
-// three workgroups per CU; eight-wave workgroups (128 rows) fit only one per
-// CU at this register count and measured slower on the packed draft block
-// (end-to-end 66.5 -> 68.9 steps/s with four).
-#ifndef D3D_ATTN_MAX_WAVES
-#define D3D_ATTN_MAX_WAVES 4
-#endif
-constexpr int kMaxWaves = D3D_ATTN_MAX_WAVES;
+// Up to 16 * kMaxWaves MFMA rows per workgroup (32 rows per wave with two
+// row tiles).  Four waves (64 rows) run three workgroups per CU; eight-wave
+// workgroups (128 rows) fit only one per CU at this register count and
+// measured slower on the packed draft block (end-to-end 66.5 -> 68.9 steps/s
+// with four).
+constexpr int kMaxWaves = 4;
 constexpr int kMaxSplitPages = 1024;  // page ids staged per split
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -85,7 +83,7 @@ struct Params {
     const int32_t* context_lens;
     uint16_t* out;
     _Float16* part_o;  // [B][nqt][Hkv][splits][M][D], O / l per split
-    float* part_ml;    // [B][nqt][Hkv][splits][M][2], (m, l) per split
+    float* part_ml;    // [B][nqt][Hkv][splits][M][4], (m, l, 2^e, 0) per split
     int B, Q, Hq, Hkv, G, M;
     int page_size, max_pages, num_pages;
     int page_shift;  // log2(page_size) for powers of two, else -1
@@ -164,6 +162,15 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     const f32x2 v = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Exponent e of the fp16 partial-output scale for a row whose largest
+// magnitude is amax: amax * 2^-e lies in [2^14, 2^15) for normal amax; e is
+// clamped to [-110, 110] so that 2^e and 2^-e are normal floats (zero,
+// subnormal, Inf and NaN rows stay finite-scaled; Inf / NaN propagate).
+__device__ __forceinline__ int row_scale_exp(float amax) {
+    const int ex = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127;
+    return min(max(ex - 14, -110), 110);
 }
 
 // Stages tokens [t0, t0 + TILE) of one KV head into registers.  Sixteen
@@ -265,7 +272,7 @@ __device__ __forceinline__ void store_tile(char* lds, const u32x4 (&reg)[2 * TIL
 // permuted V operand read from LDS feeds two MFMAs (blocks of more than 64
 // rows per KV head: the packed draft block).
 template <int NW, int MODE, bool UPG, int RT>
-__global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Params P) {
+__global__ __launch_bounds__(NW * 64, 2) void attn_split_kernel(Params P) {
     constexpr int NT = NW * 64;
     const int kvh = blockIdx.x % P.Hkv, qt = blockIdx.y;
     int b, s, nsplit, ctx;
@@ -608,27 +615,36 @@ __global__ __launch_bounds__(NW * 64, NW == 8 ? 1 : 2) void attn_split_kernel(Pa
             }
         }
     } else {
-        // Normalised partial O / l in fp16 (|O / l| <= max |v|), (m, l) in fp32.
+        // Normalised partial O / l in fp16 with a power-of-two row scale
+        // 2^e chosen so that the row's largest |O / l| lands in [2^14, 2^15):
+        // no overflow for bf16 values past fp16's 65504 and no subnormal loss
+        // for tiny ones.  (m, l, 2^e) in fp32.
         const size_t unit = (((size_t)b * P.nqt + qt) * P.Hkv + kvh) * P.num_splits + s;
         _Float16* po = P.part_o + unit * P.M * D;
-        float* pml = P.part_ml + unit * P.M * 2;
+        float4* pml = reinterpret_cast<float4*>(P.part_ml) + unit * P.M;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const float inv = l_run[rt] > 0.f ? 1.f / l_run[rt] : 0.f;
+            float amax = 0.f;
+#pragma unroll
+            for (int n = 0; n < D / 16; ++n)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) amax = fmaxf(amax, fabsf(o[rt][n][r] * inv));
+            amax = xor32_max(xor16_max(amax));  // the 4 lanes of row c16
+            const int e = row_scale_exp(amax);
+            const float down = __uint_as_float((uint32_t)(127 - e) << 23) * inv;  // 2^-e / l
             if (row[rt] < P.M) {
 #pragma unroll
                 for (int h = 0; h < D / 64; ++h)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const h16x4 v = {(_Float16)(o[rt][4 * h + 0][r] * inv), (_Float16)(o[rt][4 * h + 1][r] * inv),
-                                         (_Float16)(o[rt][4 * h + 2][r] * inv), (_Float16)(o[rt][4 * h + 3][r] * inv)};
+                        const h16x4 v = {(_Float16)(o[rt][4 * h + 0][r] * down), (_Float16)(o[rt][4 * h + 1][r] * down),
+                                         (_Float16)(o[rt][4 * h + 2][r] * down), (_Float16)(o[rt][4 * h + 3][r] * down)};
                         *reinterpret_cast<h16x4*>(po + (size_t)row[rt] * D + 64 * h + 16 * g4 + 4 * r) = v;
                     }
             }
-            if (g4 == 0 && row_ok[rt]) {
-                pml[row[rt] * 2 + 0] = m_run[rt];
-                pml[row[rt] * 2 + 1] = l_run[rt];
-            }
+            if (g4 == 0 && row_ok[rt])
+                pml[row[rt]] = make_float4(m_run[rt], l_run[rt], __uint_as_float((uint32_t)(127 + e) << 23), 0.f);
         }
     }
 }
@@ -656,15 +672,6 @@ constexpr int kMaxSplits = 256;
 // first and clamp every slot to its own split count: two round trips and no
 // stale slots (batch-8 draw 34.3 -> 32.8 us for the whole call, against the
 // exact loop's three round trips).
-#ifndef D3D_ATTN_SLOTS20
-#define D3D_ATTN_SLOTS20 1
-#endif
-#ifndef D3D_ATTN_SLOTS24
-#define D3D_ATTN_SLOTS24 1
-#endif
-#ifndef D3D_ATTN_CTX_FIRST_COMBINE
-#define D3D_ATTN_CTX_FIRST_COMBINE 1
-#endif
 constexpr int kSpecSplits = 32;
 constexpr int kSpecBatch = 4;
 
@@ -676,6 +683,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     constexpr bool SPEC = NSPEC > 0;
     __shared__ float wts[kRowsPerCombine][SPEC ? kSpecSplits : kMaxSplits];
     __shared__ float lsum[kRowsPerCombine][SPEC ? kSpecSplits : kMaxSplits];
+    __shared__ float pscale[kRowsPerCombine][SPEC ? kSpecSplits : kMaxSplits];
     __shared__ float inv_den[kRowsPerCombine];
     // Output mapping: 32 threads per row, 4 columns each.
     const int rr = threadIdx.x / 32, c4 = (threadIdx.x % 32) * 4, row = r0 + rr;
@@ -692,7 +700,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
         const int er = threadIdx.x / kSpecSplits, esp = threadIdx.x % kSpecSplits;
         const int erow = min(r0 + er, P.M - 1);
         const int esp_c = min(esp, slots - 1);
-        const float2 ml = *reinterpret_cast<const float2*>(P.part_ml + ((unit0 + esp_c) * P.M + erow) * 2);
+        const float4 ml = reinterpret_cast<const float4*>(P.part_ml)[(unit0 + esp_c) * P.M + erow];
         h16x4 hv[NSPEC > 0 ? NSPEC : 1];
 #pragma unroll
         for (int sp = 0; sp < NSPEC; ++sp) {
@@ -706,6 +714,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
         const bool live = esp < S && r0 + er < P.M;
         wts[er][esp] = live ? ml.x : -INFINITY;
         lsum[er][esp] = live ? ml.y : 0.f;
+        pscale[er][esp] = ml.z;
         __syncthreads();
         // One wave per two rows: lanes 0..31 and 32..63 fold one row each.
         {
@@ -719,7 +728,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
             float den = wgt;
 #pragma unroll
             for (int o = 16; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
-            wts[r2][l32] = wgt;  // each lane rewrites only the entry it read
+            wts[r2][l32] = wgt * pscale[r2][l32];  // each lane rewrites only the entry it read
             if (l32 == 0) inv_den[r2] = den > 0.f ? 1.f / den : 0.f;
         }
         __syncthreads();
@@ -742,14 +751,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
     // Statistics of every (row, split) in one round trip.
     for (int e = threadIdx.x; e < kRowsPerCombine * S; e += 256) {
         const int er = e / S, sp = e % S, erow = r0 + er;
-        float m = -INFINITY, l = 0.f;
+        float m = -INFINITY, l = 0.f, sc = 1.f;
         if (erow < P.M) {
-            const float2 ml = *reinterpret_cast<const float2*>(P.part_ml + ((unit0 + sp) * P.M + erow) * 2);
+            const float4 ml = reinterpret_cast<const float4*>(P.part_ml)[(unit0 + sp) * P.M + erow];
             m = ml.x;
             l = ml.y;
+            sc = ml.z;
         }
         wts[er][sp] = m;
         lsum[er][sp] = l;
+        pscale[er][sp] = sc;
     }
     __syncthreads();
     // One wave per row: lanes fold splits, then a butterfly (fixed order).
@@ -763,7 +774,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(Params P) {
             for (int sp = lane; sp < S; sp += 64) {
                 const float m = wts[r2][sp];
                 const float w = (m == -INFINITY) ? 0.f : exp2f(m - mx);
-                wts[r2][sp] = w * lsum[r2][sp];  // weight of the normalised partial O / l
+                // Weight of the stored partial (O / l) * 2^-e; the denominator
+                // takes the unscaled weight.
+                wts[r2][sp] = w * lsum[r2][sp] * pscale[r2][sp];
                 den += w * lsum[r2][sp];
             }
             for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
@@ -796,9 +809,9 @@ static void launch_slot_combine(int ns, dim3 grid, hipStream_t s, const Params& 
         hipLaunchKernelGGL((attn_combine_kernel<8, CTX_FIRST>), grid, dim3(256), 0, s, P);
     else if (ns <= 16)
         hipLaunchKernelGGL((attn_combine_kernel<16, CTX_FIRST>), grid, dim3(256), 0, s, P);
-    else if (ns <= 20 && D3D_ATTN_SLOTS20)
+    else if (ns <= 20)
         hipLaunchKernelGGL((attn_combine_kernel<20, CTX_FIRST>), grid, dim3(256), 0, s, P);
-    else if (ns <= 24 && D3D_ATTN_SLOTS24)
+    else if (ns <= 24)
         hipLaunchKernelGGL((attn_combine_kernel<24, CTX_FIRST>), grid, dim3(256), 0, s, P);
     else
         hipLaunchKernelGGL((attn_combine_kernel<32, CTX_FIRST>), grid, dim3(256), 0, s, P);
@@ -837,25 +850,21 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // the context-first combine the batch-8 optimum stays at 768: 512 / 640 /
 // 768 / 1024 / 1280 / 1536 measured 39.5 / 34.6 / 33.0 / 34.5 / 38.6 /
 // 38.7 us.
-#ifndef D3D_ATTN_TARGET_ITEMS
-#define D3D_ATTN_TARGET_ITEMS 768
-#endif
-constexpr int kTargetItems = D3D_ATTN_TARGET_ITEMS;
+constexpr int kTargetItems = 768;
 
 static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) {
     Plan p;
     const int G = Hq / Hkv;
     // Blocks of more than 64 rows per KV head (G x Q) take two row tiles per
     // wave in four-wave workgroups: 128 rows, each LDS fragment used twice.
-#ifndef D3D_ATTN_ROW_TILES
-#define D3D_ATTN_ROW_TILES 2
-#endif
-    p.rt = (kMaxWaves == 4 && G * Q > 64 && D3D_ATTN_ROW_TILES == 2) ? 2 : 1;
+    p.rt = G * Q > 64 ? 2 : 1;
     const int rows = kMaxWaves * 16 * p.rt;
     p.QT = Q < rows / G ? Q : rows / G;
     p.nqt = (Q + p.QT - 1) / p.QT;
     const int M = G * p.QT;
-    p.waves = p.rt == 2 ? 4 : (M <= 32 ? 2 : (M <= 64 ? 4 : 8));
+    // One row tile per wave: M <= 64 rows (G <= 64 is validated), so two or
+    // four waves.
+    p.waves = p.rt == 2 ? 4 : (M <= 32 ? 2 : 4);
     const int tiles = (max_context + TILE - 1) / TILE;
     // Tiles per split: about kTargetItems (request, split, kv head, query
     // tile) items if every request were max_context long.
@@ -886,7 +895,7 @@ static Plan plan(int B, int Q, int Hq, int Hkv, int max_context, int page_size) 
         p.part_o_bytes = p.part_ml_bytes = 0;
     } else {
         p.part_o_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * D * sizeof(_Float16));
-        p.part_ml_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * 2 * sizeof(float));
+        p.part_ml_bytes = align256((size_t)B * p.nqt * Hkv * p.num_splits * M * 4 * sizeof(float));
     }
     p.total = p.part_o_bytes + p.part_ml_bytes;
     if (p.total == 0) p.total = 256;
@@ -974,17 +983,13 @@ static int run(const void* q, const void* k_cache, const void* v_cache, const in
             }
             break;
         default:
-            if (upg)
-                hipLaunchKernelGGL((attn_split_kernel<8, MODE, true, 1>), grid, dim3(512), 0, s, P);
-            else
-                hipLaunchKernelGGL((attn_split_kernel<8, MODE, false, 1>), grid, dim3(512), 0, s, P);
-            break;
+            return D3D_E_UNSUPPORTED;
     }
     if (pl.num_splits > 1)
     {
         const dim3 cgrid((P.M + kRowsPerCombine - 1) / kRowsPerCombine, Hkv, B * pl.nqt);
         const int ns = pl.num_splits;
-        if (ns > kSpecSplits || (B > kSpecBatch && !D3D_ATTN_CTX_FIRST_COMBINE))
+        if (ns > kSpecSplits)
             hipLaunchKernelGGL(attn_combine_kernel<0>, cgrid, dim3(256), 0, s, P);
         else if (B > kSpecBatch)
             launch_slot_combine<true>(ns, cgrid, s, P);

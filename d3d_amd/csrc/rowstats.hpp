@@ -12,10 +12,7 @@ namespace d3d {
 namespace rows {
 
 constexpr int NT = 256;            // threads per workgroup (4 waves)
-#ifndef D3D_ROWS_CHUNK
-#define D3D_ROWS_CHUNK 4096
-#endif
-constexpr int kChunk = D3D_ROWS_CHUNK;  // vocabulary entries per chunk
+constexpr int kChunk = 4096;       // vocabulary entries per chunk
 constexpr int L = kChunk / NT;     // entries per thread per chunk
 constexpr int kMaxStatLds = 2048;  // RowStat entries staged in LDS per batch (32 KiB)
 

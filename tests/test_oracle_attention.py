@@ -109,3 +109,48 @@ def test_packed_visibility_restates_engine_mask():
             t = np.arange(S)[None, :]
             got = (t < prefix + vis[:, :1]) | ((t >= prefix + vis[:, 1:2]) & (t < prefix + vis[:, 2:3]))
             np.testing.assert_array_equal(got, engine_mask(prefix, Q, S, K, specs))
+
+
+def test_engine_mask_closed_form():
+    """engine_mask pinned by counts and intervals written from
+    serving/engine.py:35-52 directly (not from packed_visibility):
+
+    * recovery: every row sees exactly the columns [0, prefix + Q);
+    * pending rows i < K: [0, prefix + i + 1) -- the prefix and the pending
+      block causally;
+    * branch j with (accepted n, anchor) at rows K + jK .. K + jK + K - 1:
+      [0, prefix + n) plus its own block [prefix + K + jK, prefix + K + jK + K),
+      so prefix + n + K columns, and nothing of any other branch.
+    """
+    engine_mask = oa.engine_mask
+    K = 16
+    for prefix in (0, 3, 257):
+        Q, S = K, prefix + K + 5
+        m = engine_mask(prefix, Q, S, K)
+        assert (m.sum(1) == prefix + Q).all()
+        assert m[:, :prefix + Q].all() and not m[:, prefix + Q:].any()
+        for A in (1, 3):
+            specs = [(n, 100 + a) for n in range(1, K) for a in range(A)] + [(K, None)]
+            Q = K * (1 + len(specs))
+            S = prefix + Q
+            m = engine_mask(prefix, Q, S, K, specs)
+            for i in range(K):
+                row = np.zeros(S, bool)
+                row[:prefix + i + 1] = True
+                np.testing.assert_array_equal(m[i], row)
+            for j, (n, _a) in enumerate(specs):
+                off = K + j * K
+                for r in range(off, off + K):
+                    row = np.zeros(S, bool)
+                    row[:prefix + n] = True
+                    row[prefix + off:prefix + off + K] = True
+                    np.testing.assert_array_equal(m[r], row)
+                    assert m[r].sum() == prefix + n + K
+            # Branch blocks never see each other's columns.
+            own = np.zeros((Q, S), bool)
+            for j in range(len(specs)):
+                off = K + j * K
+                own[off:off + K, prefix + off:prefix + off + K] = True
+            other_blocks = np.zeros(S, bool)
+            other_blocks[prefix + K:] = True
+            assert not (m[K:] & other_blocks[None, :] & ~own[K:]).any()
