@@ -18,6 +18,8 @@ D3D_DTYPE_F32 = 0
 D3D_DTYPE_BF16 = 1
 D3D_INPUT_LOGITS = 0
 D3D_INPUT_PROBS = 1
+D3D_CONF_MAX_SOFTMAX = 0
+D3D_CONF_ONE_HOT = 1
 D3D_TOKEN_EMPTY_DISTRIBUTION = -1
 D3D_TOKEN_BAD_DRAFT = -2
 
@@ -57,17 +59,18 @@ SIGNATURES = {
     "d3d_confidence_workspace_bytes": (_SZ, [_I, _I, _I64]),
     "d3d_confidence_topk_unmask": (
         _I,
-        [_P, _I, _P, _I64, _I, _F, _I, _I, _I64, _P, _P, _P, _SZ, _P],
+        [_P, _I, _P, _I64, _I, _F, _I, _I, _F, _I, _I, _I64, _P, _P, _P, _SZ, _P],
     ),
-    "d3d_select_transfer": (_I, [_P, _I64, _I, _P, _P, _P, _I, _I, _P]),
+    "d3d_select_transfer": (_I, [_P, _I64, _I, _I, _F, _P, _P, _P, _I, _I, _P]),
     "d3d_topk_workspace_bytes": (_SZ, [_I, _I64, _I]),
     "d3d_topk_rows": (_I, [_P, _I, _I, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
     "d3d_block_inputs": (_I, [_P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "d3d_lmhead_workspace_bytes": (_SZ, [_I, _I64, _I]),
     "d3d_lmhead_topk": (_I, [_P, _P, _I, _I, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
     "d3d_sample_workspace_bytes": (_SZ, [_I, _I64]),
-    "d3d_sample_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _P, _SZ, _P]),
-    "d3d_sample_support": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "d3d_sample_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P]),
+    "d3d_softmax_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _SZ, _P]),
+    "d3d_sample_support": (_I, [_P, _P, _I, _I, _F, _F, _P, _P, _P, _P, _P]),
     "d3d_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "d3d_qk_rope_append": (
         _I,

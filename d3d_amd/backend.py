@@ -1,0 +1,237 @@
+"""Paged model runner with the reference's call surface.
+
+Mirrors serving/backend.py:
+
+* ``Runner(path, device, *, draft=False, pages=512)`` -- :24-53: one model
+  (target or draft) with its paged K/V cache and page pool on one device;
+  ``path`` names a model shape (there is no checkpoint loading: weights are
+  random-initialised bf16), see :func:`resolve_shape`;
+* ``reserve`` / ``release`` / ``trim`` / ``_tables`` -- :55-76, the page
+  bookkeeping (device-resident tables here, see model.DevicePageTables);
+* ``prefill(seqs)`` -- :98-112: the prompts' K/V and the greedy token after
+  each prompt (the target's first anchor);
+* ``forward(seqs, tokens, *, positions=None, mask_builder=None, topk=0)`` --
+  :114-136: a block of Q tokens per request after its committed prefix;
+  the target attends causally within the block, the draft under
+  ``mask_builder``'s mask (Engine._mask); returns greedy [B, Q] or
+  (top [B, Q, k], greedy [B, Q]);
+* ``verify(seqs, tokens)`` -- the target forward with the greedy acceptance
+  kernel fused after it (what Engine._verify does with the forward's greedy
+  list, serving/engine.py:133-145), returning (accepted + 1, anchor) per
+  request without a host list of the posterior.
+
+All work runs on the runner's own HIP stream (``self.stream``, a dedicated
+hardware queue) so that a target runner and a draft runner on one GPU
+overlap; block forwards are replayed from HIP graphs per (batch, block
+length, table width, mask) once seen.  Masks: a builder from
+``Engine._mask`` carries its per-query visibility descriptor; any other
+callable is evaluated and compiled to the descriptor (see
+modeling_d3d.mask_to_visibility), which must then hold for every request.
+"""
+from __future__ import annotations
+
+from typing import Dict, List, Optional, Union
+
+import torch
+
+from .draft import topk_tokens
+from .model import (D3D_1P7B, QWEN3_8B, BlockStep, ModelShape, PagedKV, Qwen3PagedModel, Sequence, block_inputs,
+                    prefill, release, reserve, trim)
+from .modeling_d3d import mask_to_visibility
+from . import speculative_sampling as ss
+from .streams import dedicated_stream
+
+PAGE = 256          # the reference's page size; ``pages`` counts pages of this size
+
+
+def _to_host(t: torch.Tensor) -> torch.Tensor:
+    """Copy into pinned host memory queued on the current stream (a pageable
+    destination would block the host until the stream drains)."""
+    buf = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    buf.copy_(t, non_blocking=True)
+    return buf
+
+
+MASK_ID = 151669
+
+# Model names the reference's command lines use (serving/bench.py:26-27),
+# mapped to their shapes.
+_SHAPES: Dict[str, ModelShape] = {
+    "Qwen/Qwen3-8B": QWEN3_8B,
+    "qwen3-8b": QWEN3_8B,
+    "fudan-generative-ai/D3D-1.7B-8B": D3D_1P7B,
+    "d3d-1.7b": D3D_1P7B,
+}
+
+
+def resolve_shape(path: Union[str, ModelShape]) -> ModelShape:
+    """The model shape a Runner builds: a ModelShape, or a known model name."""
+    if isinstance(path, ModelShape):
+        return path
+    if isinstance(path, str) and path in _SHAPES:
+        return _SHAPES[path]
+    raise ValueError(f"unknown model {path!r}: pass a ModelShape or one of {sorted(_SHAPES)}")
+
+
+class SamplingParams:
+    """serving/vendor/ssd/sampling_params.py's fields the engine sets."""
+
+    def __init__(self, temperature: float = 0.0, max_new_tokens: int = 256):
+        self.temperature = temperature
+        self.max_new_tokens = max_new_tokens
+
+
+class Runner:
+    def __init__(self, path, device="cuda:0", *, draft: bool = False, pages: int = 512, page_size: int = 16,
+                 seed: Optional[int] = None, use_graphs: bool = True):
+        self.device = torch.device(device)
+        self.draft = draft
+        shape = resolve_shape(path)
+        self.shape = shape
+        self.config = type("Config", (), dict(vocab_size=shape.vocab, num_key_value_heads=shape.kv_heads,
+                                              head_dim=shape.head_dim, hidden_size=shape.hidden,
+                                              num_hidden_layers=shape.layers))()
+        self.name = "draft" if draft else "target"
+        self.page_size = page_size
+        # ``pages`` is the reference's capacity in 256-token pages.
+        num_pages = max(1, pages * PAGE // page_size)
+        self.model = Qwen3PagedModel(shape, self.device, draft=draft, seed=(1 if draft else 0) if seed is None
+                                     else seed)
+        self.kv = PagedKV(shape, num_pages, page_size, self.device)
+        self.pool = self.kv.pool
+        self.stream = dedicated_stream(self.device)
+        self.use_graphs = use_graphs
+        self._steps: Dict = {}
+        self.width: Optional[int] = None  # fixed page-table width (graph replays), None = longest table
+
+    # -- page bookkeeping (serving/backend.py:55-76) ---------------------------
+    def table(self, seq: Sequence) -> List[int]:
+        return seq.pages.setdefault(self.name, [])
+
+    def reserve(self, seq: Sequence, length: int) -> None:
+        reserve(self.kv, seq, self.name, length)
+
+    # The device page-table pool is updated on the runner's stream, the
+    # stream every block forward reads it on.
+    def release(self, seq: Sequence) -> None:
+        if self.name in seq.pages:
+            with torch.cuda.stream(self.stream):
+                release(self.kv, seq, self.name)
+
+    def trim(self, seq: Sequence, length: int) -> None:
+        with torch.cuda.stream(self.stream):
+            trim(self.kv, seq, self.name, length)
+
+    def _tables(self, seqs: List[Sequence]) -> torch.Tensor:
+        width = max(len(self.table(s)) for s in seqs)
+        return torch.tensor([self.table(s) + [0] * (width - len(self.table(s))) for s in seqs],
+                            dtype=torch.int32, device=self.device)
+
+    @property
+    def free_pages(self) -> int:
+        return len(self.pool.free)
+
+    # -- forwards ----------------------------------------------------------------
+    @torch.inference_mode()
+    def prefill(self, seqs: List[Sequence]) -> List[int]:
+        """K/V of every prompt; the greedy next token after each prompt."""
+        nxt = self.prefill_async(seqs, tokens=True)
+        self.stream.synchronize()
+        return nxt.tolist()
+
+    @torch.inference_mode()
+    def prefill_async(self, seqs: List[Sequence], tokens: bool = False) -> Optional[torch.Tensor]:
+        """The prompts' K/V on the runner's stream, no host wait; with
+        ``tokens`` a pinned host tensor of the greedy next tokens, valid
+        once the stream has drained."""
+        with torch.cuda.stream(self.stream):
+            hidden = prefill(self.model, self.kv, seqs, self.name)
+            if not tokens:
+                return None
+            return _to_host(self.model.logits(hidden).argmax(-1))
+
+    def _inputs(self, seqs: List[Sequence], Q: int):
+        for s in seqs:
+            self.reserve(s, s.prefix + Q)
+        return block_inputs(self.kv, seqs, self.name, [s.prefix for s in seqs], Q, self.device, self.width)
+
+    def _step(self, kind: str, B: int, Q: int, width: int, vis: Optional[torch.Tensor], k: int):
+        key = (kind, B, Q, width, k, None if vis is None else tuple(map(tuple, vis.tolist())))
+        step = self._steps.get(key)
+        if step is None:
+            if kind == "verify":
+                def post(hidden, ids):
+                    out = ss.greedy_accept(self.model.logits(hidden), ids)
+                    return out.accepted, out.out_token
+            else:
+                def post(hidden, ids):
+                    top = topk_tokens(self.model.logits(hidden), max(k, 1))
+                    return top, top[..., 0]
+            step = BlockStep(self.model, self.kv, B, Q, width, causal=not self.draft, post=post,
+                             use_graph=self.use_graphs, q_vis=vis)
+            self._steps[key] = step
+        return step
+
+    @torch.inference_mode()
+    def forward(self, seqs: List[Sequence], tokens, *, positions=None, mask_builder=None, topk: int = 0,
+                host: bool = False):
+        """serving/backend.py:114-136 on the runner's stream (no host sync).
+
+        With ``host`` the results are pinned host tensors whose copies are
+        queued on the runner's stream (valid once it has drained)."""
+        with torch.cuda.stream(self.stream):
+            ids = torch.as_tensor(tokens, dtype=torch.long).to(self.device, non_blocking=True)
+            B, Q = ids.shape
+            tables, slots, lens, logical, _ = self._inputs(seqs, Q)
+            vis = None
+            if self.draft:
+                vis = self._visibility(seqs, Q, mask_builder)
+            pos = logical if positions is None else torch.as_tensor(positions).to(self.device, non_blocking=True)
+            step = self._step("forward", B, Q, tables.shape[1], vis, topk)
+            top, greedy = step(ids, pos, tables, slots, lens)
+            copy = _to_host if host else torch.clone
+            if topk:
+                return copy(top[..., :topk].contiguous()), copy(greedy)
+            return copy(greedy)
+
+    @torch.inference_mode()
+    def verify(self, seqs: List[Sequence], tokens) -> torch.Tensor:
+        """Target forward over the blocks + greedy acceptance on the device.
+
+        Returns a pinned host tensor [2, B] int64 -- commit length (accepted
+        + 1) and next anchor per request -- whose copy is queued on the
+        runner's stream (valid once it has drained)."""
+        if self.draft:
+            raise RuntimeError("verify runs on the target runner")
+        with torch.cuda.stream(self.stream):
+            ids = torch.as_tensor(tokens, dtype=torch.long).to(self.device, non_blocking=True)
+            B, Q = ids.shape
+            tables, slots, lens, logical, _ = self._inputs(seqs, Q)
+            accepted, out_token = self._step("verify", B, Q, tables.shape[1], None, 0)(ids, logical, tables,
+                                                                                       slots, lens)
+            return _to_host(torch.stack([accepted.long() + 1, out_token]))
+
+    def _visibility(self, seqs: List[Sequence], Q: int, mask_builder) -> torch.Tensor:
+        """Per-query visibility [Q, 3] (relative to the block start) of the draft mask."""
+        if mask_builder is None:
+            return torch.tensor([[Q, 0, 0]] * Q, dtype=torch.int32)  # recovery: prefix + whole block
+        desc = getattr(mask_builder, "visibility", None)
+        if desc is not None:
+            vis = desc(Q)
+            if vis.shape != (Q, 3):
+                raise ValueError("mask builder visibility must be [Q, 3]")
+            return vis.to(torch.int32)
+        # A generic builder: evaluate its [B, 1, Q, S] mask, compile it per
+        # request (each relative to its own prefix) and require one result.
+        starts = torch.tensor([s.prefix for s in seqs], device=self.device)
+        S = max(s.prefix for s in seqs) + Q
+        mask = mask_builder(starts, Q, S)
+        out = None
+        for b, s in enumerate(seqs):
+            v = mask_to_visibility(mask[b:b + 1, ..., :s.prefix + Q], Q, s.prefix + Q)
+            v = v - torch.tensor([s.prefix, s.prefix, s.prefix], dtype=torch.int32)
+            if out is None:
+                out = v
+            elif not torch.equal(out, v):
+                raise ValueError("the mask differs between requests beyond their prefixes")
+        return out

@@ -11,6 +11,7 @@ extern "C" const char* d3d_status_string(int status) {
         case D3D_E_WORKSPACE: return "workspace too small";
         case D3D_E_NULL: return "required pointer is NULL";
         case D3D_E_UNSUPPORTED: return "unsupported mode or parameter combination";
+        case D3D_E_VALUE: return "scalar argument outside its domain";
         default:
             if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
             return "unknown status";

@@ -7,10 +7,21 @@
 //       x0_p = max softmax(logits) probability
 //   third_party/sglang/python/sglang/srt/dllm/algorithm/low_confidence.py:32-35
 //       the same confidence for SGLang's LowConfidence
-// Differences, on purpose: selection is per request (the reference applies
-// row 0's indices to every row, eval_sync.py:461-464), and ties in confidence
-// go to the lowest position.  With temperature T > 1e-5 the confidence is the
-// argmax token's probability under softmax(logits / T); x0 stays the argmax.
+//   single/eval_sync.py:287-291, :323-338  greedy _sample_with_prob: the
+//       one-hot distribution, so every position's confidence is 1.0 and
+//       top-k among masked positions reduces to the tie order
+//   single/eval_sync.py:453-462  "dynamic" remasking: the masked positions
+//       with confidence >= threshold, at most k of them (the k most
+//       confident), or the plain top-k when none reaches the threshold
+// Confidence modes: D3D_CONF_MAX_SOFTMAX (the :713-717 metrics confidence,
+// SGLang's LowConfidence) or D3D_CONF_ONE_HOT (the reference's greedy
+// low_confidence steps: 1.0 everywhere, so the lowest masked positions are
+// taken first, the index order in which torch's CUDA top-k gathers tied
+// values).  Differences, on purpose: selection is per request (the
+// reference applies row 0's indices to every row, eval_sync.py:461-464), and
+// ties in confidence go to the lowest position.  With temperature T > 1e-5
+// (max-softmax mode only) the confidence is the argmax token's probability
+// under softmax(logits / T); x0 stays the argmax.
 //
 // Two kernels: row statistics of every (request, position) row, streamed once
 // in 4096-entry chunks (HBM-bound), then one workgroup per request merges the
@@ -35,6 +46,9 @@ struct Params {
     int64_t mask_id;
     int k;
     float T;
+    int one_hot;      // confidence 1.0 for every position
+    int dynamic;      // threshold remasking
+    float threshold;
     int Q, V, C;
     RowStat* stats;  // [B][Q][C]
     int64_t* x0;     // [B, Q] (may be null)
@@ -56,8 +70,15 @@ __global__ __launch_bounds__(NT) void conf_stats_kernel(Params P) {
     if (threadIdx.x == 0) P.stats[((size_t)b * P.Q + i) * P.C + c] = st;
 }
 
-// Among positions with mask[i], the k highest confidences (ties: lower
-// position; all of them when k >= their count) take x0 in block; selected
+// Number of positions to unmask: k, or with dynamic remasking the count of
+// masked positions whose confidence reaches the threshold when that count is
+// positive and below k (eval_sync.py:453-462).
+__device__ __forceinline__ int transfer_count(int k, int dynamic, int n_confident) {
+    return (dynamic && n_confident > 0) ? min(k, n_confident) : k;
+}
+
+// Among positions with mask[i], the kk highest confidences (ties: lower
+// position; all of them when kk >= their count) take x0 in block; selected
 // (may be null) records which positions were unmasked.  Rank of position i:
 // the number of masked positions with higher confidence, or equal
 // confidence and a lower index.
@@ -80,27 +101,29 @@ __device__ __forceinline__ void rank_and_unmask(int64_t* block, int Q, int k, in
 
 // Top-k unmask with caller-given tokens and confidences (the sampled draft
 // path): one workgroup per request.
-__global__ __launch_bounds__(NT) void select_transfer_kernel(int64_t* block, int64_t mask_id, int k,
-                                                             const int64_t* x0, const float* conf,
+__global__ __launch_bounds__(NT) void select_transfer_kernel(int64_t* block, int64_t mask_id, int k, int dynamic,
+                                                             float threshold, const int64_t* x0, const float* conf,
                                                              uint8_t* selected, int Q) {
     const int b = blockIdx.x;
     __shared__ float sC[kMaxQ];
     __shared__ int sX[kMaxQ];
     __shared__ uint8_t sMask[kMaxQ];
-    __shared__ int s_masked;
-    if (threadIdx.x == 0) s_masked = 0;
+    __shared__ int s_masked, s_conf;
+    if (threadIdx.x == 0) s_masked = s_conf = 0;
     __syncthreads();
-    int local = 0;
+    int local = 0, lconf = 0;
     for (int i = threadIdx.x; i < Q; i += NT) {
         const size_t e = (size_t)b * Q + i;
         sMask[i] = block[e] == mask_id;
         sC[i] = conf[e];
         sX[i] = (int)x0[e];
         local += sMask[i];
+        lconf += sMask[i] && sC[i] >= threshold;
     }
-    if (local) atomicAdd(&s_masked, local);  // LDS atomic
+    if (local) atomicAdd(&s_masked, local);  // LDS atomics
+    if (lconf) atomicAdd(&s_conf, lconf);
     __syncthreads();
-    rank_and_unmask(block + (size_t)b * Q, Q, k, s_masked, sMask, sC, sX,
+    rank_and_unmask(block + (size_t)b * Q, Q, transfer_count(k, dynamic, s_conf), s_masked, sMask, sC, sX,
                     selected ? selected + (size_t)b * Q : nullptr);
 }
 
@@ -117,21 +140,28 @@ __global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
     for (int i = threadIdx.x; i < Q; i += NT) sMask[i] = P.block[(size_t)b * Q + i] == P.mask_id;
     if (threadIdx.x == 0) s_masked = 0;
     merge_row_stats<kLogits>(P.stats + (size_t)b * Q * P.C, Q, P.C, Q, sM, sS, sArg, lds);
-    // The argmax entry's probability is exp(z_max - M) / S = 1 / S.
+    // The argmax entry's probability is exp(z_max - M) / S = 1 / S (1.0 in
+    // one-hot mode).
     for (int i = threadIdx.x; i < Q; i += NT) {
-        const float cf = 1.0f / sS[i];
+        const float cf = P.one_hot ? 1.0f : 1.0f / sS[i];
         sS[i] = cf;
         if (P.conf) P.conf[(size_t)b * Q + i] = cf;
         if (P.x0) P.x0[(size_t)b * Q + i] = sArg[i];
     }
     __syncthreads();
+    __shared__ int s_conf;
     if (threadIdx.x == 0) {
-        int n = 0;
-        for (int i = 0; i < Q; ++i) n += sMask[i];
+        int n = 0, nc = 0;
+        for (int i = 0; i < Q; ++i) {
+            n += sMask[i];
+            nc += sMask[i] && sS[i] >= P.threshold;
+        }
         s_masked = n;
+        s_conf = nc;
     }
     __syncthreads();
-    rank_and_unmask(P.block + (size_t)b * Q, Q, P.k, s_masked, sMask, sS, sArg, nullptr);
+    rank_and_unmask(P.block + (size_t)b * Q, Q, transfer_count(P.k, P.dynamic, s_conf), s_masked, sMask, sS, sArg,
+                    nullptr);
 }
 
 template <int DT, bool VEC>
@@ -153,25 +183,31 @@ extern "C" size_t d3d_confidence_workspace_bytes(int B, int Q, int64_t V) {
     return ((size_t)B * Q * conf::num_chunks(V) * sizeof(rows::RowStat) + 255) & ~(size_t)255;
 }
 
-extern "C" int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, const int64_t* x0,
-                                   const float* conf, uint8_t* selected_out, int B, int Q, void* stream) {
+extern "C" int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, int dynamic, float threshold,
+                                   const int64_t* x0, const float* conf, uint8_t* selected_out, int B, int Q,
+                                   void* stream) {
     using namespace conf;
     if (B < 1 || B > 65535 || Q < 1 || Q > kMaxQ || k < 0) return D3D_E_SHAPE;
+    if (dynamic && !(threshold == threshold)) return D3D_E_VALUE;
     if (!block_ids || !x0 || !conf) return D3D_E_NULL;
     hipLaunchKernelGGL(select_transfer_kernel, dim3(B), dim3(rows::NT), 0, static_cast<hipStream_t>(stream),
-                       block_ids, mask_id, k, x0, conf, selected_out, Q);
+                       block_ids, mask_id, k, dynamic ? 1 : 0, threshold, x0, conf, selected_out, Q);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }
 
 extern "C" int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids, int64_t mask_id,
-                                          int k, float temperature, int B, int Q, int64_t V, int64_t* x0_out,
-                                          float* conf_out, void* workspace, size_t workspace_bytes,
-                                          void* stream) {
+                                          int k, float temperature, int conf_mode, int dynamic, float threshold,
+                                          int B, int Q, int64_t V, int64_t* x0_out, float* conf_out,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
     using namespace conf;
     if (B < 1 || B > 65535 || Q < 1 || Q > kMaxQ || V < 1 || V > (int64_t)kMaxStatLds * kChunk || k < 0)
         return D3D_E_SHAPE;
     if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
+    if (conf_mode != D3D_CONF_MAX_SOFTMAX && conf_mode != D3D_CONF_ONE_HOT) return D3D_E_VALUE;
+    // One-hot confidences are the greedy draw's; a sampled draw has its own.
+    if (conf_mode == D3D_CONF_ONE_HOT && temperature > 1e-5f) return D3D_E_UNSUPPORTED;
+    if (dynamic && !(threshold == threshold)) return D3D_E_VALUE;
     if (!logits || !block_ids || !workspace) return D3D_E_NULL;
     if (workspace_bytes < d3d_confidence_workspace_bytes(B, Q, V)) return D3D_E_WORKSPACE;
     Params P;
@@ -180,6 +216,9 @@ extern "C" int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t
     P.mask_id = mask_id;
     P.k = k;
     P.T = temperature > 1e-5f ? temperature : 1.0f;
+    P.one_hot = conf_mode == D3D_CONF_ONE_HOT;
+    P.dynamic = dynamic ? 1 : 0;
+    P.threshold = threshold;
     P.Q = Q;
     P.V = (int)V;
     P.C = num_chunks(V);

@@ -2,11 +2,13 @@
 //
 // Reference behaviour (D3D repository):
 //   single/eval_sync.py:287-305  _sampling_probs: T <= 1e-5 is one-hot at
-//       the argmax, else softmax(logits / T) (top-k / top-p off)
+//       the argmax, else softmax(logits / T); top-k keeps the entries at or
+//       above the k-th largest scaled logit (ties kept, :293-295)
 //   single/eval_sync.py:308-338  _sample_tokens / _sample_with_prob: the
 //       argmax (probability 1) or a multinomial draw and its probability
 //   single/eval_sync.py:341-367  _sample_with_sparse_probs: top-S support of
-//       logits / T, softmax over the support, a draw from it
+//       logits / T, the nucleus (top-p) filter over the sorted support,
+//       softmax over the support, a draw from it
 //
 // torch.multinomial is replaced by the inverse CDF driven by one uniform u
 // per row: token = first t with C_t > u * W over the weights, else the last
@@ -36,11 +38,28 @@ struct Params {
     const void* logits;  // [N, V]
     int N, V, C;
     float T;
+    const float* kth;   // [N] top-k floor (raw logit), or null
     const float* u;     // [N]
     RowStat* stats;     // [N][C]
     int64_t* tok;       // [N]
     float* prob;        // [N] (may be null)
+    float* probs_out;   // [N, V] dense probabilities (d3d_softmax_rows)
 };
+
+// Top-k filter of _sampling_probs (single/eval_sync.py:293-295): entries
+// whose scaled logit x / T lies below the row's k-th largest scaled logit
+// kth / T become -inf (probability 0).  The division matches the
+// reference's logits.float() / T, so ties with the k-th value are kept.
+template <bool UNIT_T, int LT>
+__device__ __forceinline__ void apply_floor(const Params& P, int n, float (&x)[LT]) {
+    if (!P.kth) return;
+    const float fl = UNIT_T ? P.kth[n] : P.kth[n] / P.T;
+#pragma unroll
+    for (int j = 0; j < LT; ++j) {
+        const float z = UNIT_T ? x[j] : x[j] / P.T;
+        x[j] = z < fl ? -INFINITY : x[j];
+    }
+}
 
 template <int DT, bool VEC, Mode M, bool UNIT_T>
 __global__ __launch_bounds__(NT) void sample_stats_kernel(Params P) {
@@ -52,6 +71,7 @@ __global__ __launch_bounds__(NT) void sample_stats_kernel(Params P) {
     const int first = c * kChunk + threadIdx.x * E;
     float x[L];
     load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
+    if constexpr (M != kGreedy) apply_floor<UNIT_T>(P, n, x);
     const RowStat st = chunk_stats<DT, M, UNIT_T>(x, first, P.T, M == kGreedy, rf, ri);
     if (threadIdx.x == 0) P.stats[(size_t)n * P.C + c] = st;
 }
@@ -134,6 +154,7 @@ __global__ __launch_bounds__(NT) void sample_pick_kernel(Params P) {
             const int first = c * kChunk + tid * E;
             float x[L];
             load_tile<DT, VEC, false, L>(row, P.V, first, NT * E, -INFINITY, x);
+            apply_floor<UNIT_T>(P, n, x);
             float run = 0.f;
             int found = INT_MAX, lastpos = -1;
 #pragma unroll
@@ -181,9 +202,24 @@ __global__ __launch_bounds__(NT) void sample_pick_kernel(Params P) {
 
 // Sparse support: vals/ids [N][S] (top-S logits in descending order), one
 // wave per row: probs = softmax(vals / T) over the support, then the draw.
+__device__ __forceinline__ float wave_incl_scan(float v, int lane) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const float t = __shfl_up(v, o, kWave);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
 __global__ __launch_bounds__(NT) void support_sample_kernel(const float* __restrict__ vals,
                                                             const int64_t* __restrict__ ids, int N, int S, float T,
-                                                            const float* __restrict__ u, int64_t* tok,
+                                                            float top_p, const float* __restrict__ u, int64_t* tok,
                                                             float* probs, float* tok_prob) {
     const int lane = threadIdx.x & (kWave - 1);
     const int n = blockIdx.x * (NT / kWave) + threadIdx.x / kWave;
@@ -193,19 +229,23 @@ __global__ __launch_bounds__(NT) void support_sample_kernel(const float* __restr
     float m = z;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-    const float e = (live && z != -INFINITY) ? expf(z - m) : 0.f;
-    float Z = e;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) Z += __shfl_xor(Z, o, kWave);
-    const float p = Z > 0.f ? e / Z : 0.f;
+    float e = (live && z != -INFINITY) ? expf(z - m) : 0.f;
+    float Z = wave_sum(e);
+    float p = Z > 0.f ? e / Z : 0.f;
+    if (top_p < 1.0f) {
+        // Nucleus filter over the descending support (:356-361): entry s > 0
+        // goes when the inclusive mass of entries 0..s-1 exceeds top_p; the
+        // kept logits are renormalised (dropped ones become exactly 0).
+        const float incl = wave_incl_scan(p, lane);
+        const float before = __shfl_up(incl, 1, kWave);
+        const bool drop = lane > 0 && before > top_p;
+        e = drop ? 0.f : e;
+        Z = wave_sum(e);
+        p = Z > 0.f ? e / Z : 0.f;
+    }
     if (live) probs[(size_t)n * S + lane] = p;
     // Inclusive scan of p in support order, total W.
-    float c = p;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const float t = __shfl_up(c, o, kWave);
-        if (lane >= o) c += t;
-    }
+    const float c = wave_incl_scan(p, lane);
     const float W = __shfl(c, kWave - 1, kWave);
     const float target = u[n] * W;
     const uint64_t hit = __ballot(live && c > target && p > 0.f);
@@ -236,6 +276,77 @@ static void dispatch(const Params& P, bool greedy, hipStream_t s) {
         launch<DT, VEC, kLogits, false>(P, s);
 }
 
+// Dense probabilities: workgroup (chunk, row) merges the row's chunk
+// records in chunk order (every workgroup of the row gets the same M and W)
+// and writes p = exp(z - M) / W for its chunk, 0 for entries below the
+// top-k floor; greedy rows get the one-hot row at the argmax.
+template <int DT, bool VEC, Mode M, bool UNIT_T>
+__global__ __launch_bounds__(NT) void softmax_write_kernel(Params P) {
+    constexpr int E = Vec<DT>::E;
+    const int c = blockIdx.x, n = blockIdx.y, tid = threadIdx.x;
+    __shared__ float s_row[2];
+    __shared__ int s_arg;
+    const RowStat* src = P.stats + (size_t)n * P.C;
+    if (tid == 0) {
+        if constexpr (M == kGreedy) {
+            float bv = -INFINITY;
+            int bi = INT_MAX;
+            for (int i = 0; i < P.C; ++i) argmax_merge(bv, bi, src[i].xmax, src[i].arg);
+            s_arg = bi;
+        } else {
+            float mx = -INFINITY;
+            for (int i = 0; i < P.C; ++i) mx = fmaxf(mx, src[i].m);
+            float w = 0.f;
+            for (int i = 0; i < P.C; ++i) w += src[i].m == -INFINITY ? 0.f : src[i].s * expf(src[i].m - mx);
+            s_row[0] = mx;
+            s_row[1] = w > 0.f ? 1.0f / w : 0.f;
+        }
+    }
+    __syncthreads();
+    float* out = P.probs_out + (size_t)n * P.V;
+    const int first = c * kChunk + tid * E;
+    if constexpr (M == kGreedy) {
+        const int arg = s_arg;
+#pragma unroll
+        for (int j = 0; j < L / E; ++j)
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const int e = first + j * NT * E + k;
+                if (e < P.V) out[e] = e == arg ? 1.0f : 0.0f;
+            }
+    } else {
+        const void* row = row_ptr<DT>(P.logits, n, P.V);
+        float x[L];
+        load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
+        apply_floor<UNIT_T>(P, n, x);
+        const float Mrow = s_row[0], inv = s_row[1];
+#pragma unroll
+        for (int j = 0; j < L / E; ++j)
+#pragma unroll
+            for (int k = 0; k < E; ++k) {
+                const int e = first + j * NT * E + k;
+                const float z = UNIT_T ? x[j * E + k] : x[j * E + k] / P.T;
+                if (e < P.V) out[e] = z == -INFINITY ? 0.f : expf(z - Mrow) * inv;
+            }
+    }
+}
+
+template <int DT, bool VEC, Mode M, bool UNIT_T>
+static void launch_probs(const Params& P, hipStream_t s) {
+    hipLaunchKernelGGL((sample_stats_kernel<DT, VEC, M, UNIT_T>), dim3(P.C, P.N), dim3(NT), 0, s, P);
+    hipLaunchKernelGGL((softmax_write_kernel<DT, VEC, M, UNIT_T>), dim3(P.C, P.N), dim3(NT), 0, s, P);
+}
+
+template <int DT, bool VEC>
+static void dispatch_probs(const Params& P, bool greedy, hipStream_t s) {
+    if (greedy)
+        launch_probs<DT, VEC, kGreedy, true>(P, s);
+    else if (P.T == 1.0f)
+        launch_probs<DT, VEC, kLogits, true>(P, s);
+    else
+        launch_probs<DT, VEC, kLogits, false>(P, s);
+}
+
 }  // namespace sample
 }  // namespace d3d
 
@@ -248,8 +359,8 @@ extern "C" size_t d3d_sample_workspace_bytes(int N, int64_t V) {
 }
 
 extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
-                               const float* uniforms, int64_t* tokens_out, float* probs_out, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               const float* kth, const float* uniforms, int64_t* tokens_out, float* probs_out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
     using namespace sample;
     if (N < 0 || N > 65535 || V < 1 || V > (int64_t)rows::kMaxStatLds * rows::kChunk) return D3D_E_SHAPE;
     if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
@@ -263,6 +374,7 @@ extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, 
     P.V = (int)V;
     P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
     P.T = greedy ? 1.0f : temperature;
+    P.kth = greedy ? nullptr : kth;
     P.u = uniforms;
     P.stats = static_cast<rows::RowStat*>(workspace);
     P.tok = tokens_out;
@@ -281,18 +393,55 @@ extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, 
     return err == hipSuccess ? D3D_OK : (int)err;
 }
 
+extern "C" int d3d_softmax_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
+                                const float* kth, float* probs_out, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    using namespace sample;
+    if (N < 0 || N > 65535 || V < 1 || V > (int64_t)rows::kMaxStatLds * rows::kChunk) return D3D_E_SHAPE;
+    if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
+    if (N == 0) return D3D_OK;
+    if (!logits || !probs_out || !workspace) return D3D_E_NULL;
+    if (workspace_bytes < d3d_sample_workspace_bytes(N, V)) return D3D_E_WORKSPACE;
+    const bool greedy = !(temperature > 1e-5f);
+    Params P;
+    P.logits = logits;
+    P.N = N;
+    P.V = (int)V;
+    P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
+    P.T = greedy ? 1.0f : temperature;
+    P.kth = greedy ? nullptr : kth;
+    P.u = nullptr;
+    P.stats = static_cast<rows::RowStat*>(workspace);
+    P.tok = nullptr;
+    P.prob = nullptr;
+    P.probs_out = probs_out;
+    const size_t esize = dtype == D3D_DTYPE_F32 ? 4 : 2;
+    const bool vec = ((uintptr_t)logits % 16 == 0) && ((size_t)V * esize) % 16 == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == D3D_DTYPE_F32) {
+        if (vec) dispatch_probs<kF32, true>(P, greedy, s);
+        else dispatch_probs<kF32, false>(P, greedy, s);
+    } else {
+        if (vec) dispatch_probs<kBF16, true>(P, greedy, s);
+        else dispatch_probs<kBF16, false>(P, greedy, s);
+    }
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}
+
 extern "C" int d3d_sample_support(const float* support_vals, const int64_t* support_ids, int N, int S,
-                                  float temperature, const float* uniforms, int64_t* tokens_out,
+                                  float temperature, float top_p, const float* uniforms, int64_t* tokens_out,
                                   float* support_probs_out, float* token_probs_out, void* stream) {
     using namespace sample;
     if (N < 0 || S < 1 || S > kMaxSupport) return D3D_E_SHAPE;
     if (!(temperature > 1e-5f)) return D3D_E_UNSUPPORTED;
+    if (!(top_p > 0.f && top_p <= 1.f)) return D3D_E_VALUE;
     if (N == 0) return D3D_OK;
     if (!support_vals || !support_ids || !uniforms || !tokens_out || !support_probs_out) return D3D_E_NULL;
     const int per = rows::NT / kWave;
     hipLaunchKernelGGL(support_sample_kernel, dim3((N + per - 1) / per), dim3(rows::NT), 0,
-                       static_cast<hipStream_t>(stream), support_vals, support_ids, N, S, temperature, uniforms,
-                       tokens_out, support_probs_out, token_probs_out);
+                       static_cast<hipStream_t>(stream), support_vals, support_ids, N, S, temperature, top_p,
+                       uniforms, tokens_out, support_probs_out, token_probs_out);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }

@@ -1,27 +1,31 @@
 """Greedy speculative engine with the target and the draft on one GPU.
 
-Mirrors serving/engine.py:14-227 (the concurrent greedy engine): every step
-the target verifies each running request's block (anchor + 15 draft tokens)
-while the draft, on a second HIP stream, runs the packed multi-branch
-prediction (serving/engine.py:73-131): one forward over the pending block
-(causal: this commits the pending tokens' draft K/V) and one branch block
-per (accepted count n, anchor) outcome plus the all-accepted outcome.  A
-request whose outcome (n, anchor) was predicted takes that branch's block;
-the others are recovered by a draft forward from the new anchor
-(serving/engine.py:54-62).  The reference runs the target in another
-process on another GPU and exchanges token lists over a pipe
-(serving/target_process.py); here both models are co-resident and the
-exchange is a pair of stream events plus small device-to-host copies.
+Mirrors serving/engine.py:14-227 (the concurrent greedy engine) with the
+same constructor, methods and result dictionary:
 
-Differences from the reference, on purpose:
+* ``Engine(target, draft, block_size=16, anchor_num=3, draft_microbatch=4,
+  pages=512, backup="neural", seed=42, fast_miss_anchors=0,
+  draft_pages=None)`` -- :15-31;
+* ``_mask(specs)`` -- :35-52, the draft's recovery / packed mask builder
+  (it also carries the per-query visibility descriptor the kernels read);
+* ``_recover(seqs)`` -- :54-62, anchor + masks from the committed prefix;
+* ``_fast_backup(seqs)`` -- :64-71, random blocks for the "fast" backups;
+* ``_predict(seqs)`` -- :73-131, the packed multi-branch prediction:
+  ``{seq_id: {(n, anchor or None): (block, top)}}``;
+* ``_verify(seqs, blocks)`` / ``_accepted`` -- :133-145;
+* ``generate(prompts, concurrency, max_new_tokens=256, ignore_eos=False,
+  eos=(151643, 151645))`` -- :147-227, admission capped at
+  ``concurrency``, prefill in groups of 4, EOS and length stops, page
+  release and the leak checks.
 
-* acceptance is the fused greedy kernel on the target logits (no argmax
-  list round trip): commit length = accepted + 1, anchor = correction
-  token, exactly Engine._accepted (serving/engine.py:138-145);
-* the draft's greedy tokens and top-(A+1) anchors come from one top-k
-  kernel over the logits (serving/backend.py:84-93);
-* the packed mask is a per-query visibility descriptor read by the
-  attention kernel instead of a materialised [B, 1, Q, S] bool tensor.
+The reference runs the target in another process on another GPU
+(serving/target_process.py) and exchanges token lists over a pipe; here
+both models are co-resident, each Runner on its own HIP stream (its own
+hardware queue), so the target's verify and the draft's packed prediction
+overlap, and the exchange is a pair of stream events plus small pinned
+device-to-host copies.  Verify fuses the greedy acceptance kernel after
+the target forward (commit length and anchor come back, not the posterior
+list); its results equal Engine._accepted on the posterior.
 """
 from __future__ import annotations
 
@@ -31,63 +35,212 @@ from typing import Dict, List, Optional, Sequence as Seq, Tuple
 import torch
 
 from .attention import packed_visibility
-from .draft import MASK_ID, topk_tokens
-from . import speculative_sampling as ss
-from .streams import dedicated_stream
-from .model import (D3D_1P7B, QWEN3_8B, BlockStep, ModelShape, PagedKV, Qwen3PagedModel, Sequence, block_inputs,
-                    prefill, release, reserve, trim)
+from .backend import MASK_ID, Runner, SamplingParams
+from .model import Sequence
 
 EOS_IDS = (151643, 151645)
 
 
-def _to_host(t: torch.Tensor) -> torch.Tensor:
-    """Stream-ordered copy into pinned host memory (a pageable destination
-    would make the copy block the host until the stream drains)."""
-    buf = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
-    buf.copy_(t, non_blocking=True)
-    return buf
-
-
-def branch_specs(K: int, A: int, current: List[int], top: List[List[int]]) -> List[Tuple[int, Optional[int]]]:
-    """Engine._predict's branches (serving/engine.py:98-105): for each accepted
-    count n in 1..K-1 the first A draft top-(A+1) tokens at position n that
-    differ from current[n], then the all-accepted branch (K, None)."""
+def branch_specs(K: int, A: int, current: List[int], top: List[List[int]], shallow: bool = False,
+                 fanout: Optional[int] = None) -> List[Tuple[int, Optional[int]]]:
+    """Engine._predict's branches for one request (serving/engine.py:96-105):
+    for each accepted count n in 1..K-1 (only n = 1 when ``shallow``) the
+    first ``fanout`` (default A) tokens of the draft's top list at position n
+    that differ from current[n], then -- unless shallow -- the all-accepted
+    branch (K, None)."""
+    fanout = A if fanout is None else fanout
     out: List[Tuple[int, Optional[int]]] = []
-    for n in range(1, K):
-        anchors = [v for v in top[n] if v != current[n]][:A]
-        if len(anchors) != A:
-            raise RuntimeError("draft top-k holds fewer than A alternative anchors")
+    for n in (range(1, 2) if shallow else range(1, K)):
+        anchors = [v for v in top[n] if v != current[n]][:fanout]
+        if len(anchors) != fanout:
+            raise RuntimeError("draft top-k holds fewer alternative anchors than the fan-out")
         out.extend((n, a) for a in anchors)
-    out.append((K, None))
+    if not shallow:
+        out.append((K, None))
     return out
 
 
+class _Mask:
+    """Engine._mask's builder (serving/engine.py:35-52).
+
+    Called as ``builder(starts, Q, S)`` it returns the reference's
+    [B, 1, Q, S] bool mask; ``visibility(Q)`` gives the same mask as the
+    per-query descriptor [Q, 3] the packed attention kernel reads.
+    """
+
+    def __init__(self, K: int, specs=None):
+        self.K, self.specs = K, specs
+
+    def _accepted(self) -> Optional[List[int]]:
+        if self.specs is None:
+            return None
+        counts = [n for n, _ in self.specs[0]]
+        if any([n for n, _ in sp] != counts for sp in self.specs):
+            raise ValueError("packed branch layouts differ between requests of one microbatch")
+        return counts
+
+    def visibility(self, Q: int) -> torch.Tensor:
+        acc = self._accepted()
+        if acc is None:
+            return torch.tensor([[Q, 0, 0]] * Q, dtype=torch.int32)
+        vis = packed_visibility(self.K, acc)
+        if vis.shape[0] != Q:
+            raise ValueError("packed block length does not match the branch specs")
+        return vis
+
+    def __call__(self, starts: torch.Tensor, Q: int, S: int) -> torch.Tensor:
+        dev = starts.device
+        cols = torch.arange(S, device=dev)[None, None, :].expand(len(starts), -1, -1)
+        pref = starts[:, None, None]
+        local = cols - pref
+        if self.specs is None:
+            mask = (cols < pref + Q).expand(-1, Q, -1).clone()
+        else:
+            K = self.K
+            mask = torch.zeros(len(starts), Q, S, dtype=torch.bool, device=dev)
+            rows = torch.arange(K, device=dev)[None, :, None]
+            mask[:, :K] = (cols < pref) | ((local >= 0) & (local <= rows))
+            for b, branches in enumerate(self.specs):
+                for j, (accepted, _anchor) in enumerate(branches):
+                    off = K + j * K
+                    mask[b, off:off + K] = (cols[b] < pref[b] + accepted) | ((local[b] >= off) & (local[b] < off + K))
+        return mask[:, None]
+
+
 class Engine:
-    def __init__(self, target_shape: ModelShape = QWEN3_8B, draft_shape: ModelShape = D3D_1P7B, *,
-                 block_size: int = 16, anchor_num: int = 1, page_size: int = 16, pages: int = 4096,
-                 device: str = "cuda:0", seed: int = 42, mask_id: int = MASK_ID, use_graphs: bool = True):
-        if target_shape.vocab != draft_shape.vocab:
-            raise ValueError("target and draft vocabularies must match")
-        if not 0 <= mask_id < draft_shape.vocab:
-            raise ValueError(f"mask id {mask_id} outside the draft vocabulary")
+    def __init__(self, target, draft, block_size: int = 16, anchor_num: int = 3, draft_microbatch: int = 4,
+                 pages: int = 512, backup: str = "neural", seed: int = 42, fast_miss_anchors: int = 0,
+                 draft_pages: Optional[int] = None, *, device: str = "cuda:0", page_size: int = 16,
+                 mask_id: int = MASK_ID, use_graphs: bool = True):
+        if backup not in ("neural", "fast", "fast_legacy"):
+            raise ValueError(backup)
         if anchor_num < 1:
             raise ValueError("anchor_num must be positive")
-        self.K, self.A = block_size, anchor_num
+        if fast_miss_anchors < 0:
+            raise ValueError("fast_miss_anchors must be nonnegative")
+        if draft_microbatch < 1:
+            raise ValueError("draft_microbatch must be positive")
+        self.fast_miss_anchors = fast_miss_anchors
+        self.backup, self.seed = backup, seed
+        self.K, self.A, self.micro = block_size, anchor_num, draft_microbatch
         self.mask_id = mask_id
-        self.use_graphs = use_graphs
-        self._cache: Dict = {}
         self.device = torch.device(device)
-        self.target = Qwen3PagedModel(target_shape, self.device, draft=False, seed=seed)
-        self.draft = Qwen3PagedModel(draft_shape, self.device, draft=True, seed=seed + 1)
-        self.tkv = PagedKV(target_shape, pages, page_size, self.device)
-        self.dkv = PagedKV(draft_shape, pages, page_size, self.device)
-        # Packed prediction: the pending block + A anchors per accepted count 1..K-1 + all accepted.
-        self.nbranch = self.A * (self.K - 1) + 1
-        self.Qp = self.K * (1 + self.nbranch)
-        # Two streams at the default priority, each on its own hardware
-        # queue, so that verify and draft overlap.
-        self.ts = dedicated_stream(self.device)
-        self.ds = dedicated_stream(self.device)
+        self.target = Runner(target, self.device, pages=pages, page_size=page_size, seed=seed,
+                             use_graphs=use_graphs)
+        self.draft = Runner(draft, self.device, draft=True, pages=pages if draft_pages is None else draft_pages,
+                            page_size=page_size, seed=seed + 1, use_graphs=use_graphs)
+        if self.target.shape.vocab != self.draft.shape.vocab:
+            raise ValueError("target and draft vocabularies must match")
+        if not 0 <= mask_id < self.draft.shape.vocab:
+            raise ValueError(f"mask id {mask_id} outside the draft vocabulary")
+
+    def close(self) -> None:
+        torch.cuda.synchronize(self.device)
+
+    def _mask(self, specs=None) -> _Mask:
+        return _Mask(self.K, specs)
+
+    # -- draft side ------------------------------------------------------------
+    def _recover_submit(self, seqs: List[Sequence], topk: int):
+        """Recovery forwards (serving/engine.py:54-62) on the draft stream:
+        per microbatch the device (top, greedy) of anchor + K-1 masks."""
+        out = []
+        for off in range(0, len(seqs), self.micro):
+            group = seqs[off:off + self.micro]
+            ids = torch.full((len(group), self.K), self.mask_id, dtype=torch.long)
+            ids[:, 0] = torch.tensor([s.anchor for s in group])
+            top, greedy = self.draft.forward(group, ids, mask_builder=self._mask(), topk=topk, host=True)
+            out.append((group, top, greedy))
+        return out
+
+    def _recover(self, seqs: List[Sequence]) -> None:
+        """serving/engine.py:54-62: s.current = [anchor, draft greedy ...], s.top = top-(A+1)."""
+        for group, top, greedy in self._recover_submit(seqs, self.A + 1):
+            self.draft.stream.synchronize()
+            for s, blk, t in zip(group, greedy.tolist(), top.tolist()):
+                blk[0] = s.anchor
+                s.current, s.top = blk, t
+                s.recoveries += 1
+
+    def _fast_backup(self, seqs: List[Sequence]) -> None:
+        """serving/engine.py:64-71: a random block after the anchor (greedy
+        verification needs token ids only); the draft's masked prediction is
+        built later, in _predict."""
+        V = self.draft.shape.vocab
+        for s in seqs:
+            cur = torch.randint(V, (self.K,), generator=self.backup_rng).tolist()
+            cur[0] = s.anchor
+            s.current = cur
+            s.needs_fast_seed = True
+            s.fast_backups += 1
+
+    def _predict_submit(self, seqs: List[Sequence]):
+        """serving/engine.py:73-131 up to the packed forwards, which run on
+        the draft stream; returns what _predict_collect needs."""
+        K, A = self.K, self.A
+        missing = [s for s in seqs if s.needs_fast_seed]
+        missing_ids = {s.seq_id for s in missing}
+        miss_anchors = (self.fast_miss_anchors or A) if self.backup == "fast" else A
+        if missing:
+            for group, top, _ in self._recover_submit(missing, max(A, miss_anchors) + 1):
+                self.draft.stream.synchronize()
+                for s, t in zip(group, top.tolist()):
+                    s.top = t
+                    s.needs_fast_seed = False
+                    s.fast_seeds += 1
+        if self.backup == "fast":
+            partitions = [([s for s in seqs if s.seq_id not in missing_ids], False), (missing, True)]
+        else:
+            partitions = [(seqs, False)]
+        groups = [(part[off:off + self.micro], shallow)
+                  for part, shallow in partitions for off in range(0, len(part), self.micro)]
+        pending = []
+        for group, shallow in groups:
+            specs = [branch_specs(K, A, s.current, s.top, shallow, miss_anchors if shallow else A) for s in group]
+            Q = K + len(specs[0]) * K
+            ids = torch.full((len(group), Q), self.mask_id, dtype=torch.long)
+            pos = torch.empty_like(ids)
+            for b, s in enumerate(group):
+                ids[b, :K] = torch.tensor(s.current)
+                pos[b, :K] = torch.arange(s.prefix, s.prefix + K)
+                for j, (n, a) in enumerate(specs[b]):
+                    start = K + j * K
+                    if a is not None:
+                        ids[b, start] = a
+                    pos[b, start:start + K] = torch.arange(s.prefix + n, s.prefix + n + K)
+            top, greedy = self.draft.forward(group, ids, positions=pos, mask_builder=self._mask(specs), topk=A + 1,
+                                             host=True)
+            pending.append((group, specs, top, greedy))
+        return pending
+
+    def _predict_collect(self, pending) -> Dict[int, Dict]:
+        self.draft.stream.synchronize()
+        K = self.K
+        results: Dict[int, Dict] = {}
+        for group, specs, top, greedy in pending:
+            top_l, greedy_l = top.tolist(), greedy.tolist()
+            for b, s in enumerate(group):
+                outcomes = {}
+                for j, key in enumerate(specs[b]):
+                    start = K + j * K
+                    block = greedy_l[b][start:start + K]
+                    if key[1] is not None:
+                        block[0] = key[1]
+                    outcomes[key] = (block, top_l[b][start:start + K])
+                results[s.seq_id] = outcomes
+        return results
+
+    def _predict(self, seqs: List[Sequence]) -> Dict[int, Dict]:
+        """serving/engine.py:73-131: {seq_id: {(n, anchor or None): (block, top)}}."""
+        return self._predict_collect(self._predict_submit(seqs))
+
+    # -- target side -----------------------------------------------------------
+    def _verify(self, seqs: List[Sequence], blocks: List[List[int]]) -> List[Tuple[int, int]]:
+        """serving/engine.py:133-136: (commit length, next anchor) per request."""
+        res = self.target.verify(seqs, blocks)
+        self.target.stream.synchronize()
+        nl, al = res.tolist()
+        return list(zip(nl, al))
 
     @staticmethod
     def _accepted(blocks: List[List[int]], posterior: List[List[int]]) -> List[Tuple[int, int]]:
@@ -100,146 +253,100 @@ class Engine:
             out.append((accepted, p[accepted - 1]))
         return out
 
-    # -- graph-replayed block steps --------------------------------------------
-    def _steps(self, B: int, width: int):
-        """(verify, recovery, packed prediction) block steps for B requests, cached."""
-        key = (B, width)
-        if key not in self._cache:
-            K, k = self.K, self.A + 1
-
-            def verify_post(hidden, ids):
-                out = ss.greedy_accept(self.target.logits(hidden), ids)
-                return out.accepted, out.out_token
-
-            def recover_post(hidden, ids):
-                top = topk_tokens(self.draft.logits(hidden), k)
-                block = top[..., 0].clone()
-                block[:, 0] = ids[:, 0]
-                return block, top
-
-            def predict_post(hidden, ids):
-                return topk_tokens(self.draft.logits(hidden), k)
-
-            names = [n for n, _ in branch_specs(K, self.A, [0] * K, [list(range(1, k + 1))] * K)]
-            self._cache[key] = (
-                BlockStep(self.target, self.tkv, B, K, width, causal=True, post=verify_post,
-                          use_graph=self.use_graphs),
-                BlockStep(self.draft, self.dkv, B, K, width, causal=False, post=recover_post,
-                          use_graph=self.use_graphs),
-                BlockStep(self.draft, self.dkv, B, self.Qp, width, causal=False, post=predict_post,
-                          use_graph=self.use_graphs, q_vis=packed_visibility(K, names)),
-            )
-        return self._cache[key]
-
-    def _recover(self, seqs: List[Sequence], anchors: List[int], width: int):
-        """serving/engine.py:54-62: anchor + K-1 masks from the committed prefix;
-        returns (block [B, K], top [B, K, A+1]) on the device."""
-        ids = torch.full((len(seqs), self.K), self.mask_id, dtype=torch.int64)
-        ids[:, 0] = torch.tensor(anchors)
-        for s in seqs:
-            reserve(self.dkv, s, "draft", s.prefix + self.K)
-        tables, slots, lens, logical, _ = block_inputs(self.dkv, seqs, "draft", [s.prefix for s in seqs], self.K,
-                                                       self.device, width)
-        block, top = self._steps(len(seqs), width)[1](ids.to(self.device, non_blocking=True), logical, tables,
-                                                     slots, lens)
-        return block.clone(), top.clone()
-
-    def _predict(self, seqs: List[Sequence], current: List[List[int]], top: List[List[List[int]]], width: int):
-        """serving/engine.py:73-131, one packed forward: returns the branch
-        specs per request and the device top-(A+1) [B, Qp, A+1] of every
-        packed position (index 0 is the greedy token)."""
-        K, Qp = self.K, self.Qp
-        B = len(seqs)
-        specs = [branch_specs(K, self.A, current[b], top[b]) for b in range(B)]
-        ids = torch.full((B, Qp), self.mask_id, dtype=torch.int64)
-        pos = torch.empty((B, Qp), dtype=torch.int64)
-        for b, s in enumerate(seqs):
-            ids[b, :K] = torch.tensor(current[b])
-            pos[b, :K] = torch.arange(s.prefix, s.prefix + K)
-            for j, (n, a) in enumerate(specs[b]):
-                start = K + j * K
-                if a is not None:
-                    ids[b, start] = a
-                pos[b, start:start + K] = torch.arange(s.prefix + n, s.prefix + n + K)
-        for s in seqs:
-            reserve(self.dkv, s, "draft", s.prefix + Qp)
-        tables, slots, lens, _, _ = block_inputs(self.dkv, seqs, "draft", [s.prefix for s in seqs], Qp,
-                                                 self.device, width)
-        dev = self.device
-        out = self._steps(B, width)[2](ids.to(dev, non_blocking=True), pos.to(dev, non_blocking=True), tables,
-                                       slots, lens)
-        return specs, out.clone()
-
-    # -- main loop -----------------------------------------------------------
+    # -- the loop ----------------------------------------------------------------
     @torch.inference_mode()
-    def generate(self, prompts: Seq[Seq[int]], max_new_tokens: int = 256, ignore_eos: bool = False,
-                 eos: Tuple[int, ...] = EOS_IDS) -> Dict:
-        if max_new_tokens < 1:
-            raise ValueError("positive output length required")
-        dev = self.device
+    def generate(self, prompts: Seq[Seq[int]], concurrency: int, max_new_tokens: int = 256,
+                 ignore_eos: bool = False, eos: Tuple[int, ...] = EOS_IDS) -> Dict:
+        if concurrency < 1 or max_new_tokens < 1:
+            raise ValueError("positive concurrency and output length required")
+        K = self.K
         vocab = self.target.shape.vocab
+        prompts = [list(p) for p in prompts]
+        if any(len(p) < 1 for p in prompts):
+            raise ValueError("every prompt needs at least one token")
         if any(not 0 <= t < vocab for p in prompts for t in p):
             raise ValueError("prompt token id outside the vocabulary")
-        seqs = [Sequence(i, p) for i, p in enumerate(prompts)]
-        for s in seqs:
-            s.generated, s.accepts, s.hits, s.recoveries = [], [], 0, 0
-        # One page-table width for the whole run: the attention's context
-        # bound and the captured graphs stay fixed while contexts grow.
-        K = self.K
-        ps = self.tkv.page_size
-        width = -(-(max(len(p) for p in prompts) + max_new_tokens + self.Qp + K) // ps)
+        dev = self.device
+        self.backup_rng = torch.Generator().manual_seed(self.seed)
+        # One page-table width for the run, so the captured graphs serve
+        # every step: the longest prompt, the output, one packed block.
+        ps = self.target.page_size
+        A_max = max(self.A, self.fast_miss_anchors)
+        Qp = K * (1 + A_max * (K - 1) + 1)
+        width = -(-(max(len(p) for p in prompts) + max_new_tokens + Qp + K) // ps)
+        self.target.width = self.draft.width = width
+        waiting = iter(enumerate(prompts))
+        running: List[Sequence] = []
+        admitted_all: List[Sequence] = []
+        outputs: List[Dict] = []
+        exhausted = False
+        torch.cuda.synchronize(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
         origin = torch.cuda.Event(enable_timing=True)
         origin.record(torch.cuda.current_stream(dev))
         started = time.perf_counter()
-
-        # Prefill both models concurrently; the target's last position gives the anchor.
-        with torch.cuda.stream(self.ts):
-            h = prefill(self.target, self.tkv, seqs, "target")
-            anchor_t = self.target.logits(h).argmax(-1)
-        with torch.cuda.stream(self.ds):
-            prefill(self.draft, self.dkv, seqs, "draft")
-        self.ts.synchronize()
-        anchors = anchor_t.cpu().tolist()
-        with torch.cuda.stream(self.ds):
-            block, top = self._recover(seqs, anchors, width)
-        self.ds.synchronize()
-        for s, blk, t in zip(seqs, block.cpu().tolist(), top.cpu().tolist()):
-            s.current, s.top = blk, t
-        running = list(seqs)
+        max_active, batch_sizes = 0, []
+        miss_rounds = miss_requests = 0
         steps = 0
-        verify_ms, draft_ms, overlap_ms = [], [], []
-        timeline = []  # (verify start, end, predict start, end, recovery start, end) ms, first steps
-        outputs = []
-        while running:
+        decode_s = 0.0  # wall time of the decode steps (admission and prefill excluded)
+        verify_ms, draft_ms, overlap_ms, timeline = [], [], [], []
+        while running or not exhausted:
+            admitted = []
+            while len(running) + len(admitted) < concurrency and not exhausted:
+                try:
+                    idx, ids = next(waiting)
+                except StopIteration:
+                    exhausted = True
+                    break
+                s = Sequence(idx, ids)
+                s.sampling_params = SamplingParams(temperature=0, max_new_tokens=max_new_tokens)
+                s.index = idx
+                s.prefix = len(ids)
+                s.generated, s.accepts = [], []
+                s.born = time.perf_counter()
+                s.hits = s.recoveries = s.fast_backups = s.fast_seeds = 0
+                s.needs_fast_seed = False
+                admitted.append(s)
+                admitted_all.append(s)
+            if admitted:
+                # Prefill runs concurrently on the two streams, in groups of 4.
+                for off in range(0, len(admitted), 4):
+                    group = admitted[off:off + 4]
+                    self.draft.prefill_async(group)
+                    anchors = self.target.prefill(group)
+                    ready = []
+                    for s, a in zip(group, anchors):
+                        s.anchor = a
+                        if not ignore_eos and a in eos:
+                            s.generated = [a]
+                            self._finish(s, outputs)
+                        else:
+                            ready.append(s)
+                    self._recover(ready)
+                    running.extend(ready)
+            if not running:
+                continue
+            max_active = max(max_active, len(running))
+            batch_sizes.append(len(running))
+            t_step = time.perf_counter()
             ev = {k: torch.cuda.Event(enable_timing=True) for k in ("vs", "ve", "ps", "pe", "rs", "re")}
-            blocks = [s.current for s in running]
-            # -- target verify on ts ------------------------------------------
-            with torch.cuda.stream(self.ts):
-                ev["vs"].record(self.ts)
-                for s in running:
-                    reserve(self.tkv, s, "target", s.prefix + K)
-                tables, slots, lens, logical, _ = block_inputs(self.tkv, running, "target",
-                                                               [s.prefix for s in running], K, dev, width)
-                cur = torch.tensor(blocks, dtype=torch.int64).to(dev, non_blocking=True)
-                accepted, out_token = self._steps(len(running), width)[0](cur, logical, tables, slots, lens)
-                res = _to_host(torch.stack([accepted.long(), out_token]))
-                ev["ve"].record(self.ts)
-            # -- packed multi-branch draft prediction on ds ---------------------
-            with torch.cuda.stream(self.ds):
-                ev["ps"].record(self.ds)
-                specs, ptop = self._predict(running, blocks, [s.top for s in running], width)
-                ptop_host = _to_host(ptop)
-                ev["pe"].record(self.ds)
-            ev["ve"].synchronize()
-            ev["pe"].synchronize()
-            n_acc, tokens = res.tolist()
-            ptop_l = ptop_host.tolist()
+            blocks = [list(s.current) for s in running]
+            # Target verify on its stream ...
+            ev["vs"].record(self.target.stream)
+            res = self.target.verify(running, blocks)
+            ev["ve"].record(self.target.stream)
+            # ... while the draft predicts every outcome on its own.
+            ev["ps"].record(self.draft.stream)
+            pending = self._predict_submit(running)
+            ev["pe"].record(self.draft.stream)
+            predictions = self._predict_collect(pending)
+            self.target.stream.synchronize()
+            accepted = list(zip(*res.tolist()))
             steps += 1
-            remaining, recover, rec_anchor = [], [], []
-            for i, s in enumerate(running):
-                n = int(n_acc[i]) + 1
-                anchor = int(tokens[i])
-                emitted = blocks[i][:n][: max_new_tokens - len(s.generated)]
+            remaining, recover = [], []
+            for s, block, (n, anchor) in zip(running, blocks, accepted):
+                n, anchor = int(n), int(anchor)
+                emitted = block[:n][: max_new_tokens - len(s.generated)]
                 stop = False
                 if not ignore_eos:
                     for j, t in enumerate(emitted):
@@ -249,70 +356,133 @@ class Engine:
                 s.generated.extend(emitted)
                 s.accepts.append(n)
                 s.prefix += n
+                s.anchor = anchor
                 if stop or len(s.generated) >= max_new_tokens:
-                    outputs.append(s)
+                    self._finish(s, outputs)
                     continue
                 if not ignore_eos and anchor in eos:
                     s.generated.append(anchor)
-                    outputs.append(s)
+                    self._finish(s, outputs)
                     continue
-                trim(self.tkv, s, "target", s.prefix)
-                remaining.append(s)
                 key = (n, None if n == K else anchor)
-                j = specs[i].index(key) if key in specs[i] else -1
-                if j >= 0:
-                    rows = ptop_l[i][K + j * K: K + (j + 1) * K]
-                    s.current = [r[0] for r in rows]
-                    s.current[0] = anchor
-                    s.top = rows
-                    s.hits += 1
-                else:
-                    s.recoveries += 1
+                selected = predictions[s.seq_id].get(key)
+                if selected is None:
                     recover.append(s)
-                    rec_anchor.append(anchor)
-            for s in outputs:
-                if "target" in s.pages:
-                    release(self.tkv, s, "target")
-                if "draft" in s.pages:
-                    release(self.dkv, s, "draft")
-            if not remaining:
-                break
-            # -- misses: recovery from the new anchor ---------------------------
-            with torch.cuda.stream(self.ds):
-                ev["rs"].record(self.ds)
-                if recover:
-                    block, top = self._recover(recover, rec_anchor, width)
-                    block_host, top_host = _to_host(block), _to_host(top)
-                ev["re"].record(self.ds)
+                else:
+                    s.current, s.top = list(selected[0]), selected[1]
+                    s.current[0] = anchor
+                    s.hits += 1
+                self.target.trim(s, s.prefix)
+                self.draft.trim(s, s.prefix)
+                remaining.append(s)
+            running = remaining
+            miss_rounds += bool(recover)
+            miss_requests += len(recover)
+            ev["rs"].record(self.draft.stream)
+            if self.backup in ("fast", "fast_legacy"):
+                self._fast_backup(recover)
+            else:
+                self._recover(recover)
+            ev["re"].record(self.draft.stream)
             ev["re"].synchronize()
-            if recover:
-                for s, blk, t in zip(recover, block_host.tolist(), top_host.tolist()):
-                    s.current, s.top = blk, t
-            for s in remaining:
-                trim(self.dkv, s, "draft", s.prefix)
-            vs = origin.elapsed_time(ev["vs"])
-            ve = origin.elapsed_time(ev["ve"])
-            ps_ = origin.elapsed_time(ev["ps"])
-            pe = origin.elapsed_time(ev["pe"])
+            decode_s += time.perf_counter() - t_step
+            vs, ve = origin.elapsed_time(ev["vs"]), origin.elapsed_time(ev["ve"])
+            ps_, pe = origin.elapsed_time(ev["ps"]), origin.elapsed_time(ev["pe"])
             if len(timeline) < 8:
                 timeline.append(tuple(round(origin.elapsed_time(ev[k]), 3) for k in ("vs", "ve", "ps", "pe", "rs", "re")))
             verify_ms.append(ve - vs)
             draft_ms.append((pe - ps_) + ev["rs"].elapsed_time(ev["re"]))
             overlap_ms.append(max(0.0, min(ve, pe) - max(vs, ps_)))
-            running = remaining
         torch.cuda.synchronize(dev)
         elapsed = time.perf_counter() - started
-        outputs.sort(key=lambda s: s.seq_id)
-        total = sum(len(s.generated) for s in outputs)
-        assert len(self.tkv.pool.free) == self.tkv.num_pages, "target pages leaked"
-        assert len(self.dkv.pool.free) == self.dkv.num_pages, "draft pages leaked"
-        return dict(
-            outputs=[dict(index=s.seq_id, tokens=s.generated, accepts=s.accepts, hits=s.hits,
-                          recoveries=s.recoveries) for s in outputs],
-            elapsed_s=elapsed, output_tokens=total, tps=total / elapsed, steps=steps,
-            steps_per_s=steps / elapsed,
-            verify_ms=sum(verify_ms) / max(len(verify_ms), 1),
-            draft_ms=sum(draft_ms) / max(len(draft_ms), 1),
-            overlap_fraction=sum(overlap_ms) / max(sum(verify_ms), 1e-9),
-            timeline=timeline,
-        )
+        active = [s for s in admitted_all if "target" in s.pages]
+        assert not active, "Target sequences leaked"
+        assert self.draft.free_pages == self.draft.kv.num_pages, "Draft pages leaked"
+        assert self.target.free_pages == self.target.kv.num_pages, "Target pages leaked"
+        outputs.sort(key=lambda o: o["index"])
+        total = sum(len(o["tokens"]) for o in outputs)
+        peak = torch.cuda.max_memory_allocated(dev) / 1e9
+        return dict(outputs=outputs, elapsed_s=elapsed, output_tokens=total, tps=total / elapsed,
+                    max_active=max_active, decode_batch_sizes=batch_sizes, backup=self.backup,
+                    miss_rounds=miss_rounds, miss_requests=miss_requests,
+                    peak_allocated_gb=[peak, peak], target_active_sequences=len(active),
+                    target_free_pages=self.target.free_pages,
+                    steps=steps, decode_s=decode_s, steps_per_s=steps / max(decode_s, 1e-9),
+                    verify_ms=sum(verify_ms) / max(len(verify_ms), 1),
+                    draft_ms=sum(draft_ms) / max(len(draft_ms), 1),
+                    overlap_fraction=sum(overlap_ms) / max(sum(verify_ms), 1e-9),
+                    timeline=timeline)
+
+    def _finish(self, s: Sequence, outputs: List[Dict]) -> None:
+        outputs.append(dict(index=s.index, tokens=s.generated, latency_s=time.perf_counter() - s.born,
+                            accepts=s.accepts, hits=s.hits, recoveries=s.recoveries,
+                            fast_backups=s.fast_backups, fast_seeds=s.fast_seeds))
+        self.target.release(s)
+        self.draft.release(s)
+
+
+@torch.inference_mode()
+def generate_ar(worker: Runner, prompts: Seq[Seq[int]], concurrency: int, limit: int, eos=EOS_IDS,
+                ignore_eos: bool = False) -> Dict:
+    """Target-only greedy decoding with bounded admission and EOS refill.
+
+    serving/baseline_concurrency.py:33-90 (the reference's autoregressive
+    baseline) on a target Runner: prefill in groups of 4, then one token per
+    running request per forward.  Its tokens are what a lossless greedy
+    speculative engine must reproduce.
+    """
+    if concurrency < 1 or limit < 1 or not prompts:
+        raise ValueError("Nonempty prompts and positive concurrency/token limit required")
+    eos = set(eos)
+    started = time.perf_counter()
+    waiting = iter(enumerate(prompts))
+    running: List[Sequence] = []
+    outputs: List[Dict] = []
+    batches: List[int] = []
+    exhausted = False
+    max_active = 0
+
+    def emit(seq: Sequence, token: int) -> bool:
+        seq.generated.append(token)
+        hit_eos = (not ignore_eos) and token in eos
+        if hit_eos or len(seq.generated) >= limit:
+            outputs.append(dict(index=seq.index, tokens=seq.generated, latency_s=time.perf_counter() - seq.born,
+                                finish_reason="eos" if hit_eos else "length"))
+            worker.release(seq)
+            return True
+        return False
+
+    while running or not exhausted:
+        admitted = []
+        while len(running) + len(admitted) < concurrency and not exhausted:
+            try:
+                index, ids = next(waiting)
+            except StopIteration:
+                exhausted = True
+                break
+            seq = Sequence(index, list(ids))
+            seq.index, seq.prefix = index, len(ids)
+            seq.generated, seq.born = [], time.perf_counter()
+            admitted.append(seq)
+        max_active = max(max_active, len(running) + len(admitted))
+        for offset in range(0, len(admitted), 4):
+            group = admitted[offset:offset + 4]
+            for seq, token in zip(group, worker.prefill(group)):
+                if not emit(seq, token):
+                    running.append(seq)
+        if running:
+            batches.append(len(running))
+            nxt = worker.forward(running, [[seq.generated[-1]] for seq in running], host=True)
+            worker.stream.synchronize()
+            remaining = []
+            for seq, tokens in zip(running, nxt.tolist()):
+                seq.prefix += 1
+                if not emit(seq, int(tokens[0])):
+                    remaining.append(seq)
+            running = remaining
+    torch.cuda.synchronize(worker.device)
+    elapsed = time.perf_counter() - started
+    outputs.sort(key=lambda o: o["index"])
+    total = sum(len(o["tokens"]) for o in outputs)
+    return dict(outputs=outputs, elapsed_s=elapsed, output_tokens=total, tps=total / elapsed,
+                mean_output_tokens=total / len(outputs), max_active=max_active, decode_batch_sizes=batches)

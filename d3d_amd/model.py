@@ -21,9 +21,10 @@ Reference structure followed:
 Block attention: the target attends causally within the 16-token block
 (flash_attn_with_kvcache, serving/vendor/ssd/layers/attention.py:38-41); the
 draft block sees the prefix and the whole block (recovery mask,
-serving/engine.py:41-42).  Prompt prefill reuses the block kernel: slice j of
-16 prompt tokens is run as its own request with context 16 (j + 1), which is
-exactly causal attention over the prompt.
+serving/engine.py:41-42).  Prompt prefill reuses the block kernel: each
+prompt is cut into 16-token slices aligned to its end, and each slice runs as
+its own request whose context ends at the slice, which is exactly causal
+attention over the prompt (any prompt length).
 """
 from __future__ import annotations
 
@@ -369,19 +370,31 @@ class BlockStep:
 def prefill(model: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], name: str, block: int = 16) -> torch.Tensor:
     """Writes the prompts' K/V and returns the last prompt position's hidden state [B, hidden].
 
-    Prompt lengths must be equal multiples of ``block``: slice j of each
-    prompt runs as a request with context block * (j + 1) (causal prefill).
+    The prefill of serving/backend.py:98-112 for prompts of any lengths >= 1
+    on the block kernel: prompt b of n tokens is cut into J = ceil(n / block)
+    slices aligned to its end; slice j starts at n - block (J - j) and runs
+    as a request of ``block`` queries whose context is start + block, so
+    query i sees positions <= start + i (causal attention over the prompt).
+    Rows of the first slice before position 0 are padding: their slot is -1
+    (no K/V written) and they see no key.
     """
     dev = model.device
-    n = len(seqs[0].token_ids)
-    if any(len(s.token_ids) != n for s in seqs) or n % block:
-        raise ValueError("prefill expects equal prompt lengths that are multiples of the block size")
-    for s in seqs:
+    lens = [len(s.token_ids) for s in seqs]
+    if min(lens) < 1:
+        raise ValueError("prefill needs prompts of at least one token")
+    for s, n in zip(seqs, lens):
         reserve(kv, s, name, n)
-    J = n // block
-    ids = torch.tensor([s.token_ids for s in seqs], dtype=torch.int64).reshape(len(seqs) * J, block)
-    rows = [s for s in seqs for _ in range(J)]
-    starts = [j * block for _ in seqs for j in range(J)]
-    tables, slots, lens, logical, max_ctx = block_inputs(kv, rows, name, starts, block, dev)
-    hidden = model(ids.to(dev), logical, kv, tables, lens, slots, causal=True, max_context=max_ctx)
-    return hidden.reshape(len(seqs), n, -1)[:, -1]
+    rows, starts, ids, last = [], [], [], []
+    for s, n in zip(seqs, lens):
+        J = -(-n // block)
+        toks = s.token_ids
+        for j in range(J):
+            st = n - block * (J - j)
+            rows.append(s)
+            starts.append(st)
+            ids.append([toks[p] if p >= 0 else 0 for p in range(st, st + block)])
+        last.append(len(rows) - 1)
+    ids_t = torch.tensor(ids, dtype=torch.int64).to(dev, non_blocking=True)
+    tables, slots, ctx, logical, max_ctx = block_inputs(kv, rows, name, starts, block, dev)
+    hidden = model(ids_t, logical, kv, tables, ctx, slots, causal=True, max_context=max_ctx)
+    return hidden[torch.tensor(last, device=dev), -1]

@@ -43,6 +43,11 @@ extern "C" {
 #define D3D_E_WORKSPACE (-3)
 #define D3D_E_NULL (-4)
 #define D3D_E_UNSUPPORTED (-5)
+#define D3D_E_VALUE (-6) /* a scalar argument outside its domain (mode, threshold, top_p) */
+
+/* Confidence of a greedy draft token (d3d_confidence_topk_unmask). */
+#define D3D_CONF_MAX_SOFTMAX 0 /* softmax(logits / T')[argmax]: the metrics confidence */
+#define D3D_CONF_ONE_HOT 1     /* 1.0: the reference's greedy low_confidence steps */
 
 /* Sentinels written to out_token[b] by the acceptance kernels. */
 #define D3D_TOKEN_EMPTY_DISTRIBUTION (-1) /* the resampling weights sum to zero */
@@ -207,34 +212,41 @@ size_t d3d_confidence_workspace_bytes(int B, int Q, int64_t V);
  * One denoise iteration of the diffusion draft: greedy token and confidence
  * for every position, then top-k unmask of the masked positions, in place.
  *
- * Replaces single/eval_sync.py:447-465 (_select_transfer, low-confidence
- * remasking) with the greedy confidence of single/eval_sync.py:713-717:
- * x0 = argmax(logits), conf = softmax(logits / T')[x0] with T' = T when
- * T > 1e-5, else 1.  Among positions with block_ids == mask_id the k highest
- * confidences (ties: lowest position; all of them when k >= their count)
- * take x0.  Selection is per request.
+ * Replaces single/eval_sync.py:447-465 (_select_transfer) with x0 =
+ * argmax(logits) and, by conf_mode, either the metrics confidence of
+ * single/eval_sync.py:713-717 (D3D_CONF_MAX_SOFTMAX: conf =
+ * softmax(logits / T')[x0], T' = T when T > 1e-5, else 1) or the one-hot
+ * confidence of the greedy _sample_with_prob, single/eval_sync.py:287-291
+ * and :323-338 (D3D_CONF_ONE_HOT: conf = 1.0, greedy only, else
+ * D3D_E_UNSUPPORTED).  Among positions with block_ids == mask_id the kk
+ * highest confidences (ties: lowest position; all of them when kk >= their
+ * count) take x0, where kk = k, or with dynamic != 0 ("dynamic" remasking,
+ * single/eval_sync.py:453-462) kk = min(k, n) when n > 0 masked positions
+ * have conf >= threshold.  Selection is per request.
  *
  * logits [B, Q, V] fp32 or bf16; block_ids [B, Q] int64 (in/out);
  * x0_out [B, Q] int64 and conf_out [B, Q] fp32 may be NULL.  Q <= 1024.
  */
 int d3d_confidence_topk_unmask(const void* logits, int dtype, int64_t* block_ids, int64_t mask_id,
-                               int k, float temperature, int B, int Q, int64_t V, int64_t* x0_out,
-                               float* conf_out, void* workspace, size_t workspace_bytes,
-                               void* stream);
+                               int k, float temperature, int conf_mode, int dynamic, float threshold,
+                               int B, int Q, int64_t V, int64_t* x0_out, float* conf_out,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Top-k unmask with caller-given tokens and confidences: among positions
- * with block_ids == mask_id, the k highest conf (ties: lowest position; all
- * of them when k >= their count) take x0, in place; selected_out [B, Q]
- * uint8 (may be NULL) marks the positions unmasked.  x0 [B, Q] int64, conf
- * [B, Q] fp32, Q <= 1024.
+ * with block_ids == mask_id, the kk highest conf (ties: lowest position; all
+ * of them when kk >= their count) take x0, in place, with kk as in
+ * d3d_confidence_topk_unmask (dynamic threshold remasking when dynamic !=
+ * 0); selected_out [B, Q] uint8 (may be NULL) marks the positions unmasked.
+ * x0 [B, Q] int64, conf [B, Q] fp32, Q <= 1024.
  *
  * Replaces _select_transfer, single/eval_sync.py:447-465, when x0 and its
  * confidence come from the sampled proposal (_sample_with_prob or the
  * sparse support, single/eval_sync.py:560-576); selection is per request.
  */
-int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, const int64_t* x0,
-                        const float* conf, uint8_t* selected_out, int B, int Q, void* stream);
+int d3d_select_transfer(int64_t* block_ids, int64_t mask_id, int k, int dynamic, float threshold,
+                        const int64_t* x0, const float* conf, uint8_t* selected_out, int B, int Q,
+                        void* stream);
 
 /* Bytes of workspace d3d_topk_rows needs. */
 size_t d3d_topk_workspace_bytes(int N, int64_t V, int k);
@@ -305,31 +317,51 @@ size_t d3d_sample_workspace_bytes(int N, int64_t V);
 /*
  * One proposal token per logits row [N, V] (fp32 or bf16) and its
  * probability.  temperature <= 1e-5: the argmax (first maximum) with
- * probability 1 (uniforms unused, may be NULL).  Otherwise p =
- * softmax(logits / T) and token = the first t with C_t > u[n] * W over the
- * softmax weights, else the last t with positive weight (inverse CDF in
- * place of torch.multinomial); probs_out[n] = p[token] (may be NULL).
- * N <= 65535.  D3D_TOKEN_EMPTY_DISTRIBUTION if a row has no finite entry.
+ * probability 1 (uniforms and kth unused, may be NULL).  Otherwise p =
+ * softmax(z) over z = logits / T, restricted, when kth (may be NULL) is
+ * given, to the entries with z >= kth[n] / T (top-k filtering: kth[n] is the
+ * row's k-th largest logit, so ties with it are kept), and token = the first
+ * t with C_t > u[n] * W over the softmax weights, else the last t with
+ * positive weight (inverse CDF in place of torch.multinomial); probs_out[n]
+ * = p[token] (may be NULL).  N <= 65535.  D3D_TOKEN_EMPTY_DISTRIBUTION if a
+ * row has no finite entry.
  *
  * Replaces _sample_tokens / _sample_with_prob over _sampling_probs,
- * single/eval_sync.py:287-338 (top-k / top-p filtering off).
+ * single/eval_sync.py:287-338 (top-k filtering :293-295; top-p is served by
+ * d3d_sample_support).
  */
 int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
-                    const float* uniforms, int64_t* tokens_out, float* probs_out, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    const float* kth, const float* uniforms, int64_t* tokens_out, float* probs_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The dense proposal distribution of N logits rows [N, V]: probs_out [N, V]
+ * fp32 = softmax(logits / T) over the entries kept by the top-k floor kth
+ * (as in d3d_sample_rows; may be NULL), 0 elsewhere; temperature <= 1e-5
+ * gives the one-hot row at the argmax (first maximum).  Workspace as
+ * d3d_sample_workspace_bytes(N, V).
+ *
+ * Replaces _sampling_probs, single/eval_sync.py:287-305, where the draft
+ * keeps proposal_probs (:566-570, :577-584) for verify_speculative_block.
+ */
+int d3d_softmax_rows(const void* logits, int dtype, int N, int64_t V, float temperature, const float* kth,
+                     float* probs_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Sparse proposal over a top-S support: support_vals / support_ids [N, S]
  * are the S largest logits of each row in descending order with their ids
- * (d3d_topk_rows).  support_probs_out [N, S] = softmax(support_vals / T);
- * tokens_out[n] = support_ids[n, s] for the first s whose inclusive sum
- * exceeds u[n] * W (else the last positive entry); token_probs_out (may be
- * NULL) the drawn entry's probability.  1 <= S <= 64, temperature > 1e-5.
+ * (d3d_topk_rows).  support_probs_out [N, S] = softmax(support_vals / T),
+ * and with top_p < 1 the nucleus filter: entry s > 0 is dropped (probability
+ * 0, the rest renormalised) when the inclusive sum of the first s
+ * probabilities exceeds top_p; tokens_out[n] = support_ids[n, s] for the
+ * first s whose inclusive sum exceeds u[n] * W (else the last positive
+ * entry); token_probs_out (may be NULL) the drawn entry's probability.
+ * 1 <= S <= 64, temperature > 1e-5, 0 < top_p <= 1.
  *
  * Replaces _sample_with_sparse_probs, single/eval_sync.py:341-367.
  */
 int d3d_sample_support(const float* support_vals, const int64_t* support_ids, int N, int S,
-                       float temperature, const float* uniforms, int64_t* tokens_out,
+                       float temperature, float top_p, const float* uniforms, int64_t* tokens_out,
                        float* support_probs_out, float* token_probs_out, void* stream);
 
 /*

@@ -56,7 +56,9 @@ def _load():
         lib.oracle_accept_greedy.restype = None
         lib.oracle_accept_greedy.argtypes = [P, P, I, I, L, P, P, P, P, P]
         lib.oracle_confidence_topk.restype = None
-        lib.oracle_confidence_topk.argtypes = [P, P, ctypes.c_int64, I, D, I, I, L, P, P]
+        lib.oracle_confidence_topk.argtypes = [P, P, ctypes.c_int64, I, D, I, I, D, I, I, L, P, P]
+        lib.oracle_select_transfer.restype = None
+        lib.oracle_select_transfer.argtypes = [P, ctypes.c_int64, I, I, D, P, P, P, I]
         _lib = lib
     return _lib
 
@@ -148,16 +150,31 @@ def accept_greedy(target, tokens):
     return out
 
 
-def confidence_topk(logits, block, mask_id: int, k: int, temperature: float = 0.0):
+def confidence_topk(logits, block, mask_id: int, k: int, temperature: float = 0.0, *, one_hot: bool = False,
+                    dynamic: bool = False, threshold: float = 0.0):
     """One unmask iteration; returns (new_block, x0, conf)."""
     x = _f32(logits)
     blk = _i64(block).copy()
     B, Q, V = x.shape
     x0 = np.zeros((B, Q), np.int64)
     conf = np.zeros((B, Q), np.float32)
-    _load().oracle_confidence_topk(_p(x), _p(blk), int(mask_id), int(k), float(temperature),
-                                   B, Q, V, _p(x0), _p(conf))
+    _load().oracle_confidence_topk(_p(x), _p(blk), int(mask_id), int(k), float(temperature), int(one_hot),
+                                   int(dynamic), float(threshold), B, Q, V, _p(x0), _p(conf))
     return blk, x0, conf
+
+
+def select_transfer(block, mask_id: int, k: int, x0, conf, *, dynamic: bool = False, threshold: float = 0.0):
+    """_select_transfer per request with given x0 / conf [B, Q]; returns
+    (new_block, selected [B, Q] bool)."""
+    blk = _i64(block).copy()
+    B, Q = blk.shape
+    x0 = _i64(x0).reshape(B, Q)
+    cf = _f32(conf).reshape(B, Q)
+    sel = np.zeros((B, Q), np.uint8)
+    for b in range(B):
+        _load().oracle_select_transfer(_p(blk[b]), int(mask_id), int(k), int(dynamic), float(threshold),
+                                       _p(x0[b]), _p(cf[b]), _p(sel[b]), Q)
+    return blk, sel.astype(bool)
 
 
 def num_transfer_tokens(num_masks: int, steps: int):
@@ -167,11 +184,41 @@ def num_transfer_tokens(num_masks: int, steps: int):
     return [base + (1 if i < extra else 0) for i in range(steps)]
 
 
-def sample_with_prob(logits, temperature: float, uniforms):
+def topk_keep(x, temperature: float, top_k: int) -> np.ndarray:
+    """The top-k filter of _sampling_probs (single/eval_sync.py:292-295) on
+    one fp32 row: z = x / T in fp32 (the reference's logits.float() / T),
+    kth = the k-th largest z counting repeats (torch.topk(...).values[-1]),
+    keep z >= kth (ties with the k-th value are kept)."""
+    z = _f32(x) / np.float32(temperature)
+    if not top_k or top_k <= 0:
+        return np.ones(z.shape, bool)
+    kth = np.sort(z)[::-1][min(int(top_k), z.size) - 1]
+    return z >= kth
+
+
+def softmax_rows(logits, temperature: float, top_k: int = 0) -> np.ndarray:
+    """_sampling_probs (single/eval_sync.py:287-305) without top-p, fp64:
+    one-hot at the first argmax for T <= 1e-5, else softmax(x / T) over the
+    top-k kept entries, 0 elsewhere.  [N, V] -> [N, V]."""
+    x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
+    out = np.zeros(x.shape, np.float64)
+    for n in range(x.shape[0]):
+        if temperature <= 1e-5:
+            out[n, argmax(x[n])] = 1.0
+            continue
+        keep = topk_keep(x[n], temperature, top_k)
+        z = x[n].astype(np.float64) / temperature
+        e = np.where(keep, np.exp(z - z[keep].max()), 0.0)
+        out[n] = e / e.sum()
+    return out
+
+
+def sample_with_prob(logits, temperature: float, uniforms, top_k: int = 0):
     """single/eval_sync.py:324-338 (_sample_with_prob over _sampling_probs),
     with torch.multinomial replaced by the inverse CDF of each row's fp64
-    softmax at u[n].  Returns (tokens, probs, margins) per row of [N, V];
-    T <= 1e-5 gives the argmax with probability 1 (margin inf)."""
+    softmax at u[n] (over the top-k kept entries when top_k > 0).  Returns
+    (tokens, probs, margins) per row of [N, V]; T <= 1e-5 gives the argmax
+    with probability 1 (margin inf)."""
     x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
     u = np.asarray(uniforms, np.float64).reshape(-1)
     N = x.shape[0]
@@ -179,7 +226,7 @@ def sample_with_prob(logits, temperature: float, uniforms):
     prob = np.zeros(N, np.float64)
     margin = np.full(N, np.inf)
     for n in range(N):
-        p = row_probs(x[n], KIND_LOGITS, temperature)
+        p = softmax_rows(x[n][None], temperature, top_k)[0] if top_k else row_probs(x[n], KIND_LOGITS, temperature)
         if temperature <= 1e-5:
             tok[n] = int(np.argmax(p))
         else:
@@ -188,11 +235,12 @@ def sample_with_prob(logits, temperature: float, uniforms):
     return tok, prob, margin
 
 
-def sample_sparse(logits, temperature: float, S: int, uniforms):
+def sample_sparse(logits, temperature: float, S: int, uniforms, top_p: float = 1.0):
     """single/eval_sync.py:341-367 (_sample_with_sparse_probs), fp64: the S
     largest entries of logits / T (descending, ties by lower id), softmax over
-    them, inverse-CDF draw at u[n].  Returns (tokens, ids [N,S], probs [N,S],
-    margins)."""
+    them, the nucleus filter (entry s > 0 dropped when the inclusive mass of
+    entries 0..s-1 exceeds top_p, then renormalised), inverse-CDF draw at
+    u[n].  Returns (tokens, ids [N,S], probs [N,S], margins)."""
     x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
     u = np.asarray(uniforms, np.float64).reshape(-1)
     N, V = x.shape
@@ -207,6 +255,10 @@ def sample_sparse(logits, temperature: float, S: int, uniforms):
         e = np.exp(zs - zs.max())
         ids[n] = order
         probs[n] = e / e.sum()
+        if top_p < 1.0:
+            before = np.concatenate([[0.0], np.cumsum(probs[n])[:-1]])
+            e = np.where(before > top_p, 0.0, e)
+            probs[n] = e / e.sum()
         local, margin[n] = inverse_cdf(probs[n], u[n])
         tok[n] = order[local]
     return tok, ids, probs, margin

@@ -243,18 +243,55 @@ void oracle_accept_greedy(const float* target, const int64_t* tokens, int B, int
 }
 
 /*
+ * _select_transfer (eval_sync.py:447-465) for one request with given x0 and
+ * conf [Q]: among positions holding mask_id, the kk highest confidences
+ * (ties: lowest index) take their x0 (selection by repeated maximum); kk as
+ * in oracle_confidence_topk.  selected [Q] (may be NULL) marks them.
+ */
+void oracle_select_transfer(int64_t* blk, int64_t mask_id, int k, int dynamic, double threshold,
+                            const int64_t* x0, const float* conf, uint8_t* selected, int Q) {
+    int masked = 0, confident = 0;
+    for (int i = 0; i < Q; ++i) {
+        masked += blk[i] == mask_id;
+        confident += blk[i] == mask_id && conf[i] >= (float)threshold;
+    }
+    int kk = (dynamic && confident > 0) ? (k < confident ? k : confident) : k;
+    if (kk > masked) kk = masked;
+    if (Q <= 0) return;
+    uint8_t* taken = (uint8_t*)calloc((size_t)(unsigned)Q, 1);
+    for (int r = 0; r < kk; ++r) {
+        int best = -1;
+        for (int i = 0; i < Q; ++i) {
+            if (blk[i] != mask_id || taken[i]) continue;
+            if (best < 0 || conf[i] > conf[best]) best = i;
+        }
+        taken[best] = 1;
+    }
+    for (int i = 0; i < Q; ++i) {
+        if (taken[i]) blk[i] = x0[i];
+        if (selected) selected[i] = taken[i];
+    }
+    free(taken);
+}
+
+/*
  * Confidence and top-k unmask for one denoise iteration
  * (eval_sync.py:447-465 _select_transfer), per request rather than with row
  * 0's indices applied to every row (:461-464).
  *   logits [B, Q, V] fp32, block [B, Q] in/out.  x0 = argmax of each row and
  *   conf = its softmax(logits / T) probability, with T taken as 1 when
  *   T <= 1e-5 (the greedy confidence of eval_sync.py:713-717 and of SGLang's
- *   low_confidence.py:32-35).  Among positions holding mask_id, the k highest
- *   confidences (ties: lowest index) take their x0.  x0 [B, Q] and
- *   conf [B, Q] are written for every row.
+ *   low_confidence.py:32-35), or 1.0 with one_hot (the greedy
+ *   _sample_with_prob of eval_sync.py:287-291, :323-338).  Among positions
+ *   holding mask_id, the kk highest confidences (ties: lowest index) take
+ *   their x0; kk = k, except with dynamic remasking (eval_sync.py:453-462):
+ *   when n > 0 masked positions have conf >= threshold (compared in fp32, as
+ *   torch compares a float32 tensor with a Python float), kk = min(k, n).
+ *   x0 [B, Q] and conf [B, Q] are written for every row.
  */
 void oracle_confidence_topk(const float* logits, int64_t* block, int64_t mask_id, int k,
-                            double T, int B, int Q, long V, int64_t* x0, float* conf) {
+                            double T, int one_hot, int dynamic, double threshold, int B, int Q, long V,
+                            int64_t* x0, float* conf) {
     for (int b = 0; b < B; ++b) {
         for (int i = 0; i < Q; ++i) {
             const float* x = logits + ((size_t)b * Q + i) * V;
@@ -263,23 +300,9 @@ void oracle_confidence_topk(const float* logits, int64_t* block, int64_t mask_id
             double Te = T <= 1e-5 ? 1.0 : T;
             double m = (double)x[a] / Te, s = 0.0;
             for (long t = 0; t < V; ++t) s += exp((double)x[t] / Te - m);
-            conf[(size_t)b * Q + i] = (float)(1.0 / s);
+            conf[(size_t)b * Q + i] = one_hot ? 1.0f : (float)(1.0 / s);
         }
-        int64_t* blk = block + (size_t)b * Q;
-        int masked = 0;
-        for (int i = 0; i < Q; ++i) masked += blk[i] == mask_id;
-        int kk = k < masked ? k : masked;
-        uint8_t* taken = (uint8_t*)calloc((size_t)Q, 1);
-        for (int r = 0; r < kk; ++r) {
-            int best = -1;
-            for (int i = 0; i < Q; ++i) {
-                if (blk[i] != mask_id || taken[i]) continue;
-                if (best < 0 || conf[(size_t)b * Q + i] > conf[(size_t)b * Q + best]) best = i;
-            }
-            taken[best] = 1;
-        }
-        for (int i = 0; i < Q; ++i)
-            if (taken[i]) blk[i] = x0[(size_t)b * Q + i];
-        free(taken);
+        oracle_select_transfer(block + (size_t)b * Q, mask_id, k, dynamic, threshold, x0 + (size_t)b * Q,
+                               conf + (size_t)b * Q, NULL, Q);
     }
 }

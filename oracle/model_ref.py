@@ -64,3 +64,36 @@ def causal_then_block(prefix: int, block: int, bidirectional: bool):
     if bidirectional:
         m[prefix:, :] = True
     return m
+
+
+def random_layer(shape, seed: int = 0):
+    """fp32 weights of one decoder layer of ``shape`` (CPU), for timing."""
+    g = torch.Generator().manual_seed(seed)
+    h, d, Hq, Hkv = shape.hidden, shape.head_dim, shape.heads, shape.kv_heads
+    w = lambda *dims: torch.randn(*dims, generator=g) * 0.02
+    return dict(qkv=w((Hq + 2 * Hkv) * d, h), o=w(h, Hq * d), gate_up=w(2 * shape.mlp, h), down=w(h, shape.mlp),
+                ln1=torch.ones(h), ln2=torch.ones(h), qn=torch.ones(d), kn=torch.ones(d))
+
+
+def layer_step(L, shape, inv_freq, x, residual, pos, k_past, v_past, mask):
+    """One decoder layer (the op sequence of ``forward``) over new rows x
+    [T, h] attending to cached keys/values [P, Hkv, d] plus their own, under
+    mask [T, P + T]; returns (x, residual) for the next layer."""
+    Hq, Hkv, d = shape.heads, shape.kv_heads, shape.head_dim
+    residual = x if residual is None else residual + x
+    hs = _rms(residual, L["ln1"], shape.eps)
+    q, k, v = (hs @ L["qkv"].T).split([Hq * d, Hkv * d, Hkv * d], -1)
+    q = _rope(_rms(q.reshape(-1, Hq, d), L["qn"], shape.eps), pos, inv_freq)
+    k = _rope(_rms(k.reshape(-1, Hkv, d), L["kn"], shape.eps), pos, inv_freq)
+    v = v.reshape(-1, Hkv, d)
+    k = torch.cat([k_past, k])
+    v = torch.cat([v_past, v])
+    G = Hq // Hkv
+    kk = k.repeat_interleave(G, 1).transpose(0, 1)
+    vv = v.repeat_interleave(G, 1).transpose(0, 1)
+    o = F.scaled_dot_product_attention(q.transpose(0, 1), kk, vv, attn_mask=mask, scale=d ** -0.5)
+    x = o.transpose(0, 1).reshape(-1, Hq * d) @ L["o"].T
+    residual = residual + x
+    hs = _rms(residual, L["ln2"], shape.eps)
+    gate, up = (hs @ L["gate_up"].T).chunk(2, -1)
+    return (F.silu(gate) * up) @ L["down"].T, residual

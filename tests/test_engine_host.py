@@ -1,11 +1,14 @@
-"""Host-side logic of the engine step (CPU): branch specs and acceptance lists."""
+"""Host-side logic of the engine step (CPU): branch specs, acceptance lists,
+the packed mask builder and constructor validation."""
 from __future__ import annotations
 
 import random
 
 import pytest
+import torch
 
-from d3d_amd.engine import Engine, branch_specs
+from d3d_amd.engine import Engine, _Mask, branch_specs
+from d3d_amd.modeling_d3d import mask_to_visibility
 
 
 def _reference_specs(K, A, current, top):
@@ -31,6 +34,14 @@ def test_branch_specs_follow_engine_predict(A):
     assert len(branch_specs(K, A, current, top)) == A * (K - 1) + 1
 
 
+def test_shallow_branches():
+    """serving/engine.py:98-104 with shallow=True: only n = 1, fan-out
+    miss_anchors, no all-accepted branch."""
+    top = [[7, 8, 9, 10]] * 4
+    current = [1, 8, 2, 3]
+    assert branch_specs(4, 1, current, top, shallow=True, fanout=3) == [(1, 7), (1, 9), (1, 10)]
+
+
 def test_branch_specs_need_enough_alternatives():
     with pytest.raises(RuntimeError):
         branch_specs(3, 2, [1, 2, 3], [[1, 2, 3], [2, 2, 2], [5, 6, 7]])
@@ -41,3 +52,44 @@ def test_accepted_lists_follow_engine_accepted():
     assert Engine._accepted([[5, 1, 2, 9]], [[1, 2, 7, 8]]) == [(3, 7)]
     assert Engine._accepted([[5, 1, 2]], [[1, 2, 4]]) == [(3, 4)]
     assert Engine._accepted([[5, 0, 0]], [[1, 2, 4]]) == [(1, 1)]
+
+
+@pytest.mark.parametrize("A", [1, 3])
+def test_mask_builder_visibility_equals_its_mask(A):
+    """_Mask's bool mask (serving/engine.py:35-52) and its descriptor agree,
+    for the recovery mask and the packed mask, at several prefixes."""
+    K = 16
+    specs = [(n, 100 + a) for n in range(1, K) for a in range(A)] + [(K, None)]
+    Q = K * (1 + len(specs))
+    for builder, q in ((_Mask(K), K), (_Mask(K, [specs, specs]), Q)):
+        starts = torch.tensor([0, 37])
+        S = 37 + q
+        mask = builder(starts, q, S)
+        vis = builder.visibility(q)
+        for b, p in enumerate(starts.tolist()):
+            got = mask_to_visibility(mask[b:b + 1, ..., :p + q], q, p + q)
+            rel = vis + torch.tensor([p, p, p], dtype=torch.int32)
+            # empty second ranges may be written as any lo == hi
+            empty = got[:, 1] == got[:, 2]
+            assert torch.equal(got[:, 0], rel[:, 0])
+            assert torch.equal(got[~empty, 1:], rel[~empty, 1:])
+            assert ((rel[empty, 1] == rel[empty, 2]) | (rel[empty, 2] <= rel[empty, 0])).all()
+
+
+def test_mask_to_visibility_rejects_other_shapes():
+    m = torch.zeros(1, 1, 2, 10, dtype=torch.bool)
+    m[0, 0, 0, [0, 1, 4, 8]] = True  # three runs
+    with pytest.raises(ValueError):
+        mask_to_visibility(m, 2, 10)
+    m2 = torch.ones(2, 1, 2, 10, dtype=torch.bool)
+    m2[1, 0, 0, 9] = False  # differs between requests
+    with pytest.raises(ValueError):
+        mask_to_visibility(m2, 2, 10)
+    assert mask_to_visibility(None, 3, 7).tolist() == [[7, 0, 0]] * 3
+
+
+@pytest.mark.parametrize("kw", [dict(backup="slow"), dict(anchor_num=0), dict(fast_miss_anchors=-1),
+                                dict(draft_microbatch=0)])
+def test_engine_rejects_bad_arguments_before_allocating(kw):
+    with pytest.raises(ValueError):
+        Engine("Qwen/Qwen3-8B", "fudan-generative-ai/D3D-1.7B-8B", **kw)

@@ -106,3 +106,72 @@ def test_exact_ties_go_to_lower_id_and_position(T, dtype):
     np.testing.assert_array_equal(blk, ref_blk)
     assert list(np.flatnonzero(blk[0] != MASK)) == [3, 7]
     assert list(np.flatnonzero(blk[1] != MASK)) == [0, 1]
+
+
+@pytest.mark.parametrize("V", [1000, 151936])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_hot_confidence_takes_lowest_masked_positions(V, dtype):
+    """The reference's greedy low_confidence step: every confidence is 1.0
+    (single/eval_sync.py:287-291, :323-338), so the k lowest masked
+    positions of each request take their argmax."""
+    logits, block = _case(V + 5, 4, 16, V, 11)
+    dev = torch.device("cuda:0")
+    lg = logits.to(dtype)
+    blk = block.to(dev)
+    x0, conf = draft.confidence_topk_unmask(lg.to(dev), blk, MASK, 4, 0.0, confidence="sampled")
+    torch.cuda.synchronize()
+    ref_blk, ref_x0, ref_conf = oracle.confidence_topk(lg.float().numpy(), block.numpy(), MASK, 4, 0.0,
+                                                       one_hot=True)
+    assert (conf.cpu().numpy() == 1.0).all() and (ref_conf == 1.0).all()
+    np.testing.assert_array_equal(x0.cpu().numpy(), ref_x0)
+    np.testing.assert_array_equal(blk.cpu().numpy(), ref_blk)
+    for b in range(4):
+        masked = np.flatnonzero(block[b].numpy() == MASK)
+        assert (blk.cpu().numpy()[b][masked[:4]] != MASK).all() and (blk.cpu().numpy()[b][masked[4:]] == MASK).all()
+
+
+@pytest.mark.parametrize("threshold", [0.05, 0.3, 0.9, 2.0])
+@pytest.mark.parametrize("confidence", ["max_softmax", "sampled"])
+def test_dynamic_remasking_vs_oracle(threshold, confidence):
+    """single/eval_sync.py:453-462: the masked positions whose confidence
+    reaches the threshold (at most k), or the plain top-k when none does;
+    requests are selected independently."""
+    V = 4099
+    g = torch.Generator().manual_seed(int(threshold * 100))
+    logits = torch.randn(6, 16, V, generator=g) * torch.linspace(0.5, 9.0, 16)[None, :, None]
+    block = torch.full((6, 16), MASK, dtype=torch.int64)
+    block[:, ::5] = 3
+    dev = torch.device("cuda:0")
+    blk = block.to(dev)
+    x0, conf = draft.confidence_topk_unmask(logits.to(dev), blk, MASK, 5, 0.0, confidence=confidence,
+                                            remasking="low_confidence_dynamic", threshold=threshold)
+    torch.cuda.synchronize()
+    ref_blk, ref_x0, ref_conf = oracle.confidence_topk(logits.numpy(), block.numpy(), MASK, 5, 0.0,
+                                                       one_hot=confidence == "sampled", dynamic=True,
+                                                       threshold=threshold)
+    np.testing.assert_array_equal(x0.cpu().numpy(), ref_x0)
+    # rows whose confidences sit within rounding of the threshold or of each other are left out
+    c = ref_conf
+    near = (np.abs(c - threshold) < 1e-5 * np.maximum(c, 1e-30)).any(-1)
+    if confidence == "sampled":
+        ok = ~near  # every confidence is exactly 1.0: ties by position, nothing to certify
+    else:
+        ok = ~near & _certified(ref_conf, block.numpy(), 5)
+    assert ok.mean() >= 0.5
+    np.testing.assert_array_equal(blk.cpu().numpy()[ok], ref_blk[ok])
+
+
+def test_select_transfer_dynamic_vs_oracle():
+    g = torch.Generator().manual_seed(8)
+    B, Q = 5, 24
+    block = torch.where(torch.rand(B, Q, generator=g) < 0.7, MASK, 4)
+    x0 = torch.randint(0, 100, (B, Q), generator=g)
+    conf = torch.round(torch.rand(B, Q, generator=g) * 10) / 10  # many ties
+    dev = torch.device("cuda:0")
+    for thr in (0.0, 0.65, 0.95, 1.5):
+        blk = block.clone().to(dev)
+        sel = draft.select_transfer(blk, MASK, 6, x0.to(dev), conf.to(dev), remasking="dynamic", threshold=thr)
+        ref_blk, ref_sel = oracle.select_transfer(block.numpy(), MASK, 6, x0.numpy(), conf.numpy(), dynamic=True,
+                                                  threshold=thr)
+        np.testing.assert_array_equal(blk.cpu().numpy(), ref_blk)
+        np.testing.assert_array_equal(sel.cpu().numpy(), ref_sel)

@@ -1,19 +1,28 @@
-"""End-to-end greedy speculative loop (GPU).
+"""End-to-end greedy speculative loop (GPU), called as serving/bench.py calls it.
 
 Greedy speculative decoding is lossless: whatever the draft proposes, each
 committed token is the target's greedy token given the tokens before it.
-The check feeds the engine's own output to the fp32 CPU restatement of the
-target (teacher forcing) and requires every token to be the restatement's
-argmax wherever its top-2 logit margin exceeds 5 % of the logit standard
-deviation (closer margins are near ties that bf16 rounding may decide
-either way); at least half of the positions must be decisive.
+Checks:
+
+* teacher forcing against the fp32 CPU restatement of the target: every
+  token is the restatement's argmax wherever its top-2 logit margin
+  exceeds 5 % of the logit standard deviation (closer margins are near ties
+  that bf16 rounding may decide either way), on at least half the
+  positions;
+* equality with target-only greedy decoding on the same HIP model
+  (generate_ar, serving/baseline_concurrency.py), up to a first divergence
+  that must sit at such a near tie;
+* the reference's Engine surface: positional ``concurrency``, admission
+  capped at it, ragged prompts, EOS stops, the ``fast`` / ``fast_legacy``
+  backups, ``_predict``'s outcome dictionary and ``_verify`` against
+  ``_accepted`` on the target's posterior; no page leaks.
 """
 from __future__ import annotations
 
-import torch
 import pytest
+import torch
 
-from d3d_amd.engine import Engine
+from d3d_amd.engine import Engine, generate_ar
 from d3d_amd.model import ModelShape
 from oracle import model_ref
 
@@ -23,17 +32,40 @@ TARGET = ModelShape(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=128, mlp
 DRAFT = ModelShape(layers=1, hidden=256, heads=4, kv_heads=2, head_dim=128, mlp=256, vocab=1000)
 
 
+def _engine(seed, **kw):
+    eng = Engine(TARGET, DRAFT, pages=16, seed=seed, mask_id=999, **kw)
+    for r in (eng.target, eng.draft):
+        r.model.lm_head.mul_(20.0)  # logits with std ~6: top-2 margins far above rounding
+    return eng
+
+
+def _near_tie(W, prompt, tokens, i):
+    """Is the target's top-2 margin at generated position i a near tie?"""
+    ids = list(prompt) + list(tokens[:i])
+    T = len(ids)
+    logits = model_ref.forward(W, TARGET, torch.tensor(ids), torch.arange(T), torch.ones(T, T).tril().bool())[-1]
+    top2 = logits.topk(2).values
+    return float(top2[0] - top2[1]) <= 0.05 * float(logits.std())
+
+
+def _same_up_to_near_tie(W, prompts, a, b):
+    for p, x, y in zip(prompts, a, b):
+        if x == y:
+            continue
+        i = next(j for j in range(min(len(x), len(y))) if x[j] != y[j])
+        assert _near_tie(W, p, x, i), f"outputs diverge at a decisive position {i}"
+
+
 def test_engine_output_is_target_greedy_decoding():
-    eng = Engine(TARGET, DRAFT, pages=256, seed=7, mask_id=999)
-    for m in (eng.target, eng.draft):
-        m.lm_head.mul_(20.0)  # logits with std ~6: top-2 margins far above rounding
+    eng = _engine(7)
     g = torch.Generator().manual_seed(3)
     prompts = torch.randint(0, 999, (2, 32), generator=g).tolist()
     new = 40
-    res = eng.generate(prompts, max_new_tokens=new, ignore_eos=True)
+    res = eng.generate(prompts, 2, max_new_tokens=new, ignore_eos=True)
     assert [len(o["tokens"]) for o in res["outputs"]] == [new, new]
     assert res["steps"] >= 1 and 0.0 <= res["overlap_fraction"] <= 1.0
-    W = model_ref.weights_fp32(eng.target)
+    assert res["target_active_sequences"] == 0 and res["target_free_pages"] == eng.target.kv.num_pages
+    W = model_ref.weights_fp32(eng.target.model)
     for o, p in zip(res["outputs"], prompts):
         ids = list(p)
         decisive = 0
@@ -47,23 +79,124 @@ def test_engine_output_is_target_greedy_decoding():
                 decisive += 1
             ids.append(t)  # teacher forcing with the engine's own tokens
         assert decisive >= new // 2
-    # Engine._accepted keeps the reference's list semantics.
-    assert Engine._accepted([[5, 1, 2, 9]], [[1, 2, 7, 8]]) == [(3, 7)]
-    assert Engine._accepted([[5, 1, 2]], [[1, 2, 4]]) == [(3, 4)]
+    ar = generate_ar(eng.target, prompts, 2, new, ignore_eos=True)
+    _same_up_to_near_tie(W, prompts, [o["tokens"] for o in ar["outputs"]], [o["tokens"] for o in res["outputs"]])
 
 
 def test_graph_replay_matches_eager_engine():
     """Every step replayed from HIP graphs gives the eager run's tokens."""
     outs = []
     for graphs in (False, True):
-        eng = Engine(TARGET, DRAFT, pages=256, seed=11, mask_id=999, use_graphs=graphs)
-        for m in (eng.target, eng.draft):
-            m.lm_head.mul_(20.0)
+        eng = _engine(11, use_graphs=graphs)
         g = torch.Generator().manual_seed(4)
         prompts = torch.randint(0, 999, (3, 48), generator=g).tolist()
-        res = eng.generate(prompts, max_new_tokens=30, ignore_eos=True)
+        res = eng.generate(prompts, 3, max_new_tokens=30, ignore_eos=True)
         outs.append([o["tokens"] for o in res["outputs"]])
         # a second run on the same engine replays the cached graphs again
-        res2 = eng.generate(prompts, max_new_tokens=30, ignore_eos=True)
+        res2 = eng.generate(prompts, 3, max_new_tokens=30, ignore_eos=True)
         assert [o["tokens"] for o in res2["outputs"]] == outs[-1]
     assert outs[0] == outs[1]
+
+
+def test_admission_ragged_prompts_and_eos():
+    """Five prompts of lengths 1..45 at concurrency 2: no more than two run
+    at once, every prompt is served in index order of the outputs; an EOS
+    id stops a request right after it (inclusive) and the rest keep going."""
+    eng = _engine(13)
+    g = torch.Generator().manual_seed(5)
+    lens = [1, 17, 45, 16, 30]
+    prompts = [torch.randint(0, 999, (n,), generator=g).tolist() for n in lens]
+    res = eng.generate(prompts, 2, max_new_tokens=24, ignore_eos=True)
+    assert res["max_active"] <= 2 and max(res["decode_batch_sizes"]) <= 2
+    assert [o["index"] for o in res["outputs"]] == list(range(5))
+    assert all(len(o["tokens"]) == 24 for o in res["outputs"])
+    W = model_ref.weights_fp32(eng.target.model)
+    ar = generate_ar(eng.target, prompts, 2, 24, ignore_eos=True)
+    _same_up_to_near_tie(W, prompts, [o["tokens"] for o in ar["outputs"]], [o["tokens"] for o in res["outputs"]])
+    first = res["outputs"][2]["tokens"]
+    stop = first[5]
+    j = first.index(stop)  # the first occurrence ends the request
+    res2 = eng.generate(prompts, 2, max_new_tokens=24, ignore_eos=False, eos=(stop,))
+    out2 = res2["outputs"][2]["tokens"]
+    assert out2 == first[:j + 1]
+    for o in res2["outputs"]:
+        assert stop not in o["tokens"][:-1]
+
+
+@pytest.mark.parametrize("backup", ["fast", "fast_legacy"])
+def test_fast_backups_stay_lossless(backup):
+    """Random backup blocks change what is verified, not what is committed."""
+    g = torch.Generator().manual_seed(6)
+    prompts = torch.randint(0, 999, (3, 20), generator=g).tolist()
+    ref = _engine(17)
+    want = ref.generate(prompts, 3, max_new_tokens=20, ignore_eos=True)
+    eng = _engine(17, backup=backup, fast_miss_anchors=2 if backup == "fast" else 0)
+    got = eng.generate(prompts, 3, max_new_tokens=20, ignore_eos=True)
+    assert got["backup"] == backup
+    assert sum(o["fast_backups"] for o in got["outputs"]) >= 1
+    W = model_ref.weights_fp32(eng.target.model)
+    _same_up_to_near_tie(W, prompts, [o["tokens"] for o in want["outputs"]], [o["tokens"] for o in got["outputs"]])
+
+
+def test_predict_and_verify_surfaces():
+    """_predict returns {seq_id: {(n, anchor or None): (block, top)}} with A
+    branches per accepted count and the all-accepted one; _verify equals
+    _accepted on the target's greedy posterior."""
+    from d3d_amd.model import Sequence
+    eng = _engine(19, anchor_num=2)
+    g = torch.Generator().manual_seed(7)
+    seqs = []
+    for i, n in enumerate((20, 33)):
+        s = Sequence(i, torch.randint(0, 999, (n,), generator=g).tolist())
+        s.prefix = n
+        s.needs_fast_seed = False
+        s.recoveries = 0
+        seqs.append(s)
+    anchors = eng.target.prefill(seqs)
+    eng.draft.prefill(seqs)
+    for s, a in zip(seqs, anchors):
+        s.anchor = a
+    eng._recover(seqs)
+    assert all(len(s.current) == 16 and s.current[0] == s.anchor and len(s.top) == 16 for s in seqs)
+    pred = eng._predict(seqs)
+    for s in seqs:
+        keys = list(pred[s.seq_id])
+        assert len(keys) == 2 * 15 + 1 and keys[-1] == (16, None)
+        for (n, a), (block, top) in pred[s.seq_id].items():
+            assert len(block) == 16 and len(top) == 16 and len(top[0]) == 3
+            if a is not None:
+                assert block[0] == a and a != s.current[n]
+    blocks = [list(s.current) for s in seqs]
+    got = eng._verify(seqs, blocks)
+    posterior = eng.target.forward(seqs, blocks).cpu().tolist()
+    assert got == Engine._accepted(blocks, posterior)
+    for s in seqs:
+        eng.target.release(s)
+        eng.draft.release(s)
+    assert eng.target.free_pages == eng.target.kv.num_pages and eng.draft.free_pages == eng.draft.kv.num_pages
+
+
+def test_generic_mask_builder_equals_descriptor():
+    """Runner.forward compiles a plain mask callable (the reference's
+    Engine._mask closure) to the same per-query visibility the engine's
+    builder carries."""
+    from d3d_amd.model import Sequence
+    eng = _engine(23, anchor_num=1)
+    g = torch.Generator().manual_seed(8)
+    seqs = []
+    for i in range(2):
+        s = Sequence(i, torch.randint(0, 999, (40,), generator=g).tolist())
+        seqs.append(s)
+    eng.draft.prefill(seqs)
+    K = 16
+    specs = [[(n, 5) for n in range(1, K)] + [(K, None)]] * 2
+    Q = K * (1 + len(specs[0]))
+    ids = torch.randint(0, 999, (2, Q), generator=g)
+    builder = eng._mask(specs)
+    a_top, a_g = eng.draft.forward(seqs, ids, mask_builder=builder, topk=2)
+
+    def plain(starts, Q_, S):
+        return builder(starts, Q_, S)
+
+    b_top, b_g = eng.draft.forward(seqs, ids, mask_builder=plain, topk=2)
+    assert torch.equal(a_top, b_top) and torch.equal(a_g, b_g)

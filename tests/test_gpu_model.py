@@ -110,12 +110,13 @@ def test_denoise_loop_matches_restatement():
                 checked += 1
     assert checked >= 4
     # The loop gives the same block as the steps above.
-    again = dr.d3d_draft_block(model, kv, seqs, torch.full((2, 16), mask_id, dtype=torch.int64, device=dev), 4,
-                               mask_id=mask_id)
+    again = dr.draft_block_step(model, kv, seqs, torch.full((2, 16), mask_id, dtype=torch.int64, device=dev), 4,
+                                mask_id=mask_id, confidence="max_softmax")
     assert torch.equal(again, cur)
 
 
-def test_denoise_graph_replay_matches_eager():
+@pytest.mark.parametrize("confidence", ["max_softmax", "sampled"])
+def test_denoise_graph_replay_matches_eager(confidence):
     dev = torch.device("cuda:0")
     model = Qwen3PagedModel(TINY, dev, draft=True, seed=9, init_std=0.05)
     model.lm_head.mul_(20.0)
@@ -125,37 +126,41 @@ def test_denoise_graph_replay_matches_eager():
     prefill(model, kv, seqs, "draft")
     mask_id = TINY.vocab - 1
     block = torch.full((2, 16), mask_id, dtype=torch.int64, device=dev)
-    eager = dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id)
+    eager = dr.draft_block_step(model, kv, seqs, block, 4, mask_id=mask_id, confidence=confidence)
     graphs = {}
     for _ in range(3):  # capture, then replays with eager work in between
-        got = dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id, graphs=graphs)
+        got = dr.draft_block_step(model, kv, seqs, block, 4, mask_id=mask_id, confidence=confidence, graphs=graphs)
         torch.cuda.synchronize()
         assert torch.equal(got, eager)
-        assert torch.equal(dr.d3d_draft_block(model, kv, seqs, block, 4, mask_id=mask_id), eager)
+        assert torch.equal(dr.draft_block_step(model, kv, seqs, block, 4, mask_id=mask_id, confidence=confidence),
+                           eager)
 
 
 @pytest.mark.parametrize("mode", ["block_causal", "causal"])
 def test_fused_commit_matches_restatement(mode):
-    """single/eval_sync.py:596-775: pending tokens committed to the draft cache
-    in the same forward as the anchor block (mask of :251-275), top-2
-    log-probabilities of the last step, then a later block that reads the
-    committed K/V."""
+    """single/eval_sync.py:596-775 called with the reference's parameters:
+    pending tokens committed to the draft cache in the same forward as the
+    anchor block (mask of :251-275), top-2 log-probabilities of the last
+    step, then a later block that reads the committed K/V."""
+    from d3d_amd.modeling_d3d import D3DForCausalLM
     dev = torch.device("cuda:0")
     model = Qwen3PagedModel(TINY, dev, draft=True, seed=13, init_std=0.05)
+    drafter = D3DForCausalLM(TINY, dev, pages=64, model=model)
     model.lm_head.mul_(20.0)
-    kv = PagedKV(TINY, 64, 16, dev)
     g = torch.Generator().manual_seed(6)
     mask_id = TINY.vocab - 1
     prompts = torch.randint(0, mask_id, (2, 32), generator=g)
     pending = torch.randint(0, mask_id, (2, 5), generator=g)
-    seqs = [Sequence(i, p.tolist()) for i, p in enumerate(prompts)]
-    prefill(model, kv, seqs, "draft")
-    for s in seqs:
-        s.prefix += 5  # committed, K/V not written yet
+    cache = drafter.new_cache(2)
+    drafter.prefill(cache, prompts.to(dev))
+    assert cache.get_seq_length() == 32
     block = torch.full((2, 16), mask_id, dtype=torch.int64)
     block[:, 0] = torch.tensor([3, 4])
-    cur, metrics = dr.d3d_draft_block_fused_commit(model, kv, seqs, block.to(dev), pending.to(dev), 1,
-                                                   mask_id=mask_id, attention_mask_mode=mode, return_topk=2)
+    cur, metrics = dr.d3d_draft_block_fused_commit(
+        drafter, block.to(dev), draft_kv=cache, draft_kv_len=32, pending_commit=pending.to(dev), prefix_len=37,
+        denoising_steps=1, remasking="low_confidence", threshold=0.9, temperature=0.0, top_k=0, top_p=1.0,
+        mask_id=mask_id, attention_mask_mode=mode, return_topk=2)
+    assert cache.get_seq_length() == 37
     W = model_ref.weights_fp32(model)
     T = 32 + 5 + 16
     for b in range(2):
@@ -178,9 +183,13 @@ def test_fused_commit_matches_restatement(mode):
         # one step: every mask takes the greedy token, the anchor stays
         assert cur[b, 0].item() == block[b, 0].item()
         assert torch.equal(cur[b, 1:].cpu()[sure[1:]], ref.argmax(-1)[1:][sure[1:]])
-    # A later block reads the committed pending K/V.
+    # A later block reads the committed pending K/V (the draft model's call
+    # surface, store_kv=False, with the reference's _full_mask).
     nxt = torch.randint(0, mask_id, (2, 16), generator=g)
-    got = dr.draft_block_forward(model, kv, seqs, nxt.to(dev), "draft")
+    out = drafter(nxt.to(dev), attention_mask=torch.ones(1, 1, 16, 37 + 16, dtype=torch.bool, device=dev),
+                  position_ids=torch.arange(37, 53, device=dev)[None], past_key_values=cache, use_cache=True,
+                  store_kv=False, logits_to_keep=16)
+    assert cache.get_seq_length() == 37
     for b in range(2):
         ids = torch.cat([prompts[b], pending[b], nxt[b]])
         mask = torch.ones(T, T).tril().bool()
@@ -188,4 +197,6 @@ def test_fused_commit_matches_restatement(mode):
             mask[32:37, :37] = True
         mask[37:, :] = True
         ref = model_ref.forward(W, TINY, ids, torch.arange(T), mask)[37:]
-        _close(got[b], ref)
+        _close(out.logits[b], ref)
+    cache.release()
+    assert len(drafter.kv.pool.free) == drafter.kv.num_pages

@@ -119,11 +119,12 @@ def test_select_transfer_matches_ranking(Q, k):
 TINY = ModelShape(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=128, mlp=512, vocab=1000)
 
 
-@pytest.mark.parametrize("proposal", ["logits", "sparse"])
-def test_stochastic_denoise_loop_plumbing(proposal):
+@pytest.mark.parametrize("proposal,top_k", [("logits", 0), ("probs", 16), ("sparse", 16)])
+def test_stochastic_denoise_loop_plumbing(proposal, top_k):
     """The sampled denoise loop equals its steps run one by one: the forward,
-    the draw at that step's uniforms, the top-k unmask, the last step filling
-    every mask, and proposals recorded at the step a position is unmasked."""
+    the draw at that step's uniforms (top-k filtered when top_k > 0), the
+    top-k unmask, the last step filling every mask, and proposals recorded
+    at the step a position is unmasked."""
     model = Qwen3PagedModel(TINY, DEV, draft=True, seed=5, init_std=0.05)
     T, steps, S = 0.9, 4, 16
     g = torch.Generator().manual_seed(1)
@@ -139,8 +140,8 @@ def test_stochastic_denoise_loop_plumbing(proposal):
         return kv, seqs
 
     kv, seqs = fresh()
-    got, prop = dr.d3d_draft_block(model, kv, seqs, block.to(DEV), steps, mask_id=999, temperature=T, top_k=S,
-                                   name="d", uniforms=u.to(DEV), return_proposal=proposal)
+    got, prop = dr.draft_block_step(model, kv, seqs, block.to(DEV), steps, mask_id=999, temperature=T,
+                                    top_k=top_k, name="d", uniforms=u.to(DEV), return_proposal=proposal)
     kv, seqs = fresh()
     cur = block.clone().to(DEV)
     sched = dr.get_num_transfer_tokens(15, steps)
@@ -152,14 +153,51 @@ def test_stochastic_denoise_loop_plumbing(proposal):
             x0, ids, probs = dr.sample_with_sparse_probs(logits, T, S, uniforms=u[step].to(DEV))
             conf = probs.gather(-1, (ids == x0[..., None]).long().argmax(-1, keepdim=True))[..., 0]
         else:
-            x0, conf = dr.sample_with_prob(logits, T, uniforms=u[step].to(DEV))
+            x0, conf = dr.sample_with_prob(logits, T, top_k, uniforms=u[step].to(DEV))
         sel = dr.select_transfer(cur, 999, k, x0, conf)
         for b, i in sel.nonzero().tolist():
-            rows[(b, i)] = logits[b, i].clone() if proposal == "logits" else (ids[b, i].clone(), probs[b, i].clone())
+            if proposal == "logits":
+                rows[(b, i)] = logits[b, i].clone()
+            elif proposal == "probs":
+                rows[(b, i)] = dr.sampling_probs(logits, T, top_k)[b, i].clone()
+            else:
+                rows[(b, i)] = (ids[b, i].clone(), probs[b, i].clone())
     assert torch.equal(got, cur) and not (got == 999).any()
     for (b, i), r in rows.items():
-        if proposal == "logits":
-            assert torch.equal(prop[b, i], r)
-        else:
+        if proposal == "sparse":
             assert torch.equal(prop[0][b, i], r[0]) and torch.equal(prop[1][b, i], r[1])
+        else:
+            assert torch.equal(prop[b, i], r)
     assert len(rows) == 30
+
+
+@pytest.mark.parametrize("V,top_k", [(1000, 5), (151936, 64), (151936, 1)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_top_k_filtered_sampling_vs_oracle(V, top_k, dtype):
+    """_sampling_probs' top-k filter (single/eval_sync.py:292-295): only
+    entries at or above the k-th largest scaled logit carry probability
+    (bf16 rows hold ties with the k-th value, all kept); draws and their
+    probabilities match the fp64 oracle on certified rows."""
+    N, T = 24, 0.8
+    x = _logits(V + top_k, N, V, dtype)
+    u = torch.rand(N, generator=torch.Generator().manual_seed(top_k))
+    tok, prob = dr.sample_with_prob(x.to(DEV), T, top_k, uniforms=u.to(DEV))
+    dense = dr.sampling_probs(x.to(DEV), T, top_k)
+    torch.cuda.synchronize()
+    rt, rp, margin = oracle.sample_with_prob(x.float().numpy(), T, u.numpy(), top_k=top_k)
+    rd = oracle.softmax_rows(x.float().numpy(), T, top_k)
+    np.testing.assert_array_equal(dense.cpu().numpy() > 0, rd > 0)
+    np.testing.assert_allclose(dense.cpu().numpy(), rd, rtol=2e-5, atol=1e-8)
+    ok = margin > CDF_MARGIN
+    assert ok.mean() >= 0.8
+    np.testing.assert_array_equal(tok.cpu().numpy()[ok], rt[ok])
+    np.testing.assert_allclose(prob.cpu().numpy()[ok], rp[ok], rtol=2e-5, atol=1e-9)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_probs_vs_oracle(dtype):
+    x = _logits(77, 6, 151936, dtype)
+    for T in (1.0, 0.6, 0.0):
+        got = dr.sampling_probs(x.to(DEV), T)
+        ref = oracle.softmax_rows(x.float().numpy(), T)
+        np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=2e-5, atol=1e-9)
