@@ -18,6 +18,7 @@ D3D_DTYPE_F32 = 0
 D3D_DTYPE_BF16 = 1
 D3D_INPUT_LOGITS = 0
 D3D_INPUT_PROBS = 1
+D3D_ACCEPT_NOALLOC_SCRATCH_BYTES = 4 << 20
 D3D_CONF_MAX_SOFTMAX = 0
 D3D_CONF_ONE_HOT = 1
 D3D_TOKEN_EMPTY_DISTRIBUTION = -1
@@ -37,6 +38,10 @@ SIGNATURES = {
     "d3d_accept_fused": (
         _I,
         [_P, _P, _I, _I, _P, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
+    "d3d_accept_fused_noalloc": (
+        _I,
+        [_P, _P, _I, _I, _P, _P, _P, _F, _I, _I, _I64, _P, _P, _P, _P, _P, _P],
     ),
     "d3d_accept_fused_sparse": (
         _I,

@@ -43,6 +43,8 @@
 // inverse CDF over the unnormalised weights driven by resample_u:
 // token = first t with C_t > u * W, else the last t with positive weight.
 #include "d3d_common.hpp"
+
+#include <mutex>
 #include "rowstats.hpp"
 #include "../../include/d3d_hip.h"
 
@@ -707,6 +709,47 @@ static int run(const void* target, const void* draft, const int64_t* q_ids, cons
 }  // namespace accept
 }  // namespace d3d
 
+// Scratch of d3d_accept_fused_noalloc: one copy per GPU, held until the
+// process ends.  In host code the name is a stand-in for the symbol, not a
+// device address: the address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) unsigned char scratch[D3D_ACCEPT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (the current
+// device for the null stream), looked up once per device with that device
+// current.
+int scratch_address(void* stream, void** out) {
+    int dev = 0;
+    hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return D3D_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = 0;
+        e = hipGetDevice(&cur);
+        if (e != hipSuccess) return (int)e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t r = hipSetDevice(cur);
+            if (e == hipSuccess) e = r;
+        }
+        if (e != hipSuccess) return (int)e;
+        if (!p) return D3D_E_NULL;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return D3D_OK;
+}
+
+}  // namespace
+
 using namespace d3d;
 
 extern "C" size_t d3d_accept_workspace_bytes(int B, int K, int64_t V) {
@@ -735,4 +778,21 @@ extern "C" int d3d_accept_fused_sparse(const void* target, int dtype, int input_
     return accept::run(target, nullptr, q_ids, q_probs, S, dtype, input_kind, draft_tokens, uniforms, resample_u,
                        temperature, B, K, V, accepted, accept_mask, out_token, all_accepted, posterior, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" int d3d_accept_fused_noalloc(const void* target, const void* draft, int dtype, int input_kind,
+                                        const int64_t* draft_tokens, const float* uniforms,
+                                        const float* resample_u, float temperature, int B, int K, int64_t V,
+                                        int32_t* accepted, uint8_t* accept_mask, int64_t* out_token,
+                                        uint8_t* all_accepted, int64_t* posterior, void* stream) {
+    if (B < 1 || K < 1 || V < 1) return D3D_E_SHAPE;
+    // Sizes whose workspace would not fit the static scratch are refused
+    // before anything is launched.
+    if (accept::layout(B, K, V).total > (size_t)D3D_ACCEPT_NOALLOC_SCRATCH_BYTES) return D3D_E_WORKSPACE;
+    void* ws = nullptr;
+    const int st = scratch_address(stream, &ws);
+    if (st != D3D_OK) return st;
+    return accept::run(target, draft, nullptr, nullptr, 0, dtype, input_kind, draft_tokens, uniforms, resample_u,
+                       temperature, B, K, V, accepted, accept_mask, out_token, all_accepted, posterior, ws,
+                       (size_t)D3D_ACCEPT_NOALLOC_SCRATCH_BYTES, stream);
 }

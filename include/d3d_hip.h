@@ -125,6 +125,32 @@ int d3d_accept_fused_sparse(const void* target, int dtype, int input_kind,
                             int64_t* out_token, uint8_t* all_accepted, int64_t* posterior,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the static scratch d3d_accept_fused_noalloc uses on each GPU. */
+#define D3D_ACCEPT_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/*
+ * d3d_accept_fused without a caller workspace and without any allocation:
+ * the same kernels, arguments and outputs, with the row statistics kept in
+ * a file-scope device array of D3D_ACCEPT_NOALLOC_SCRATCH_BYTES (4 MiB) that
+ * each GPU the library runs on holds until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ *
+ * Sizes whose workspace (d3d_accept_workspace_bytes(B, K, V)) exceeds the
+ * scratch return D3D_E_WORKSPACE before anything is launched: at K = 15 and
+ * V = 151,936 that is B > 196.  The scratch needs no clearing between calls.
+ * The first call on a device looks the array's address up (once per
+ * device, with that device current); make it before any graph capture.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (different streams, or different threads) race.
+ */
+int d3d_accept_fused_noalloc(const void* target, const void* draft, int dtype, int input_kind,
+                             const int64_t* draft_tokens, const float* uniforms,
+                             const float* resample_u, float temperature, int B, int K, int64_t V,
+                             int32_t* accepted, uint8_t* accept_mask, int64_t* out_token,
+                             uint8_t* all_accepted, int64_t* posterior, void* stream);
+
 /*
  * Bytes of workspace the paged attention entry points need (split-context
  * partials).  max_context bounds every context_lens[b]; the same value must
