@@ -325,6 +325,15 @@ class BlockStep:
         self.graph = None
         self.out = None
         self.workspaces: list = []
+        from .streams import register_graph_owner
+        register_graph_owner(self)
+
+    def release(self) -> None:
+        """Drop the captured graph, its outputs and its workspaces (the next
+        call captures again)."""
+        self.graph = None
+        self.out = None
+        self.workspaces.clear()
 
     def _body(self):
         hidden = self.model(self.ids, self.pos, self.kv, self.tables, self.lens, self.slots, causal=self.causal,

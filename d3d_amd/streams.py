@@ -1,4 +1,4 @@
-"""HIP streams with a hardware queue of their own.
+"""HIP streams with a hardware queue of their own, and the process-exit teardown.
 
 HIP maps a process's streams onto a small set of hardware queues
 (GPU_MAX_HW_QUEUES, 4 by default); two streams that land on one queue run
@@ -6,15 +6,67 @@ their work one after the other.  The engine's verify and draft streams must
 overlap, so they are created with hipExtStreamCreateWithCUMask: a stream
 with a CU mask gets a dedicated hardware queue.  The mask enables every CU
 (no partitioning) and the streams keep the default priority.
+
+Teardown: HIP objects this package creates -- the dedicated streams and the
+HIP graphs captured by model.BlockStep, with their workspaces -- are
+released by an interpreter-exit hook, in order (drain the devices, drop the
+graphs and their memory, destroy the streams), while the HIP runtime and
+any attached tool are still fully up, instead of being left to the
+runtime's own static destruction.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
-from typing import Optional
+import weakref
+from typing import List, Optional
 
 import torch
 
 _hip: Optional[ctypes.CDLL] = None
+_streams: List[int] = []            # raw handles of the dedicated streams
+_graph_owners: "weakref.WeakSet" = weakref.WeakSet()
+_hook_registered = False
+
+
+def register_graph_owner(owner) -> None:
+    """An object with a ``release()`` that drops its captured graphs and
+    their memory; called at interpreter exit before the streams go."""
+    _ensure_hook()
+    _graph_owners.add(owner)
+
+
+def _ensure_hook() -> None:
+    global _hook_registered
+    if not _hook_registered:
+        atexit.register(teardown)
+        _hook_registered = True
+
+
+def teardown() -> None:
+    """Release captured graphs and destroy the dedicated streams (idempotent)."""
+    try:
+        if not torch.cuda.is_initialized():
+            return
+        for d in range(torch.cuda.device_count()):
+            torch.cuda.synchronize(d)
+    except Exception:
+        return
+    for owner in list(_graph_owners):
+        try:
+            owner.release()
+        except Exception:
+            pass
+    _graph_owners.clear()
+    try:
+        torch.cuda.synchronize()
+    except Exception:
+        pass
+    if _streams:
+        hip = _runtime()
+        while _streams:
+            handle = _streams.pop()
+            hip.hipStreamDestroy(ctypes.c_void_p(handle))
 
 
 def _runtime() -> ctypes.CDLL:
@@ -24,6 +76,8 @@ def _runtime() -> ctypes.CDLL:
         _hip.hipExtStreamCreateWithCUMask.restype = ctypes.c_int
         _hip.hipExtStreamCreateWithCUMask.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint32,
                                                       ctypes.POINTER(ctypes.c_uint32)]
+        _hip.hipStreamDestroy.restype = ctypes.c_int
+        _hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
     return _hip
 
 
@@ -31,7 +85,7 @@ def dedicated_stream(device) -> torch.cuda.ExternalStream:
     """A default-priority stream on its own hardware queue, covering all CUs.
 
     The stream lives until the process ends (graphs replayed on it may
-    outlive any one owner).
+    outlive any one owner); the exit hook destroys it.
     """
     device = torch.device(device)
     n = torch.cuda.get_device_properties(device).multi_processor_count
@@ -44,4 +98,6 @@ def dedicated_stream(device) -> torch.cuda.ExternalStream:
         status = _runtime().hipExtStreamCreateWithCUMask(ctypes.byref(handle), words, mask)
     if status != 0:
         raise RuntimeError(f"hipExtStreamCreateWithCUMask failed with HIP error {status}")
+    _ensure_hook()
+    _streams.append(handle.value)
     return torch.cuda.ExternalStream(handle.value, device=device)
