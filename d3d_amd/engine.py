@@ -137,6 +137,27 @@ class Engine:
     def close(self) -> None:
         torch.cuda.synchronize(self.device)
 
+    # -- failure propagation ---------------------------------------------------
+    def _drain(self) -> None:
+        """Wait for both streams, ignoring their errors (a failed step is
+        being reported already)."""
+        for r in (self.target, self.draft):
+            try:
+                r.stream.synchronize()
+            except Exception:
+                pass
+
+    def _side(self, side: str, fn, *args, **kw):
+        """Run one side's call; a failure there (a launch or argument error,
+        or a host error around it) drains both streams and surfaces as a
+        RuntimeError naming the side, as the reference's target worker
+        errors do (serving/target_process.py:82-96)."""
+        try:
+            return fn(*args, **kw)
+        except Exception as exc:
+            self._drain()
+            raise RuntimeError(f"{side} step failed: {exc}") from exc
+
     def _mask(self, specs=None) -> _Mask:
         return _Mask(self.K, specs)
 
@@ -312,8 +333,8 @@ class Engine:
                 # Prefill runs concurrently on the two streams, in groups of 4.
                 for off in range(0, len(admitted), 4):
                     group = admitted[off:off + 4]
-                    self.draft.prefill_async(group)
-                    anchors = self.target.prefill(group)
+                    self._side("draft", self.draft.prefill_async, group)
+                    anchors = self._side("target", self.target.prefill, group)
                     ready = []
                     for s, a in zip(group, anchors):
                         s.anchor = a
@@ -322,7 +343,7 @@ class Engine:
                             self._finish(s, outputs)
                         else:
                             ready.append(s)
-                    self._recover(ready)
+                    self._side("draft", self._recover, ready)
                     running.extend(ready)
             if not running:
                 continue
@@ -333,14 +354,14 @@ class Engine:
             blocks = [list(s.current) for s in running]
             # Target verify on its stream ...
             ev["vs"].record(self.target.stream)
-            res = self.target.verify(running, blocks)
+            res = self._side("target", self.target.verify, running, blocks)
             ev["ve"].record(self.target.stream)
             # ... while the draft predicts every outcome on its own.
             ev["ps"].record(self.draft.stream)
-            pending = self._predict_submit(running)
+            pending = self._side("draft", self._predict_submit, running)
             ev["pe"].record(self.draft.stream)
-            predictions = self._predict_collect(pending)
-            self.target.stream.synchronize()
+            predictions = self._side("draft", self._predict_collect, pending)
+            self._side("target", self.target.stream.synchronize)
             accepted = list(zip(*res.tolist()))
             steps += 1
             remaining, recover = [], []
@@ -382,7 +403,7 @@ class Engine:
             if self.backup in ("fast", "fast_legacy"):
                 self._fast_backup(recover)
             else:
-                self._recover(recover)
+                self._side("draft", self._recover, recover)
             ev["re"].record(self.draft.stream)
             ev["re"].synchronize()
             decode_s += time.perf_counter() - t_step

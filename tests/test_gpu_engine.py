@@ -200,3 +200,32 @@ def test_generic_mask_builder_equals_descriptor():
 
     b_top, b_g = eng.draft.forward(seqs, ids, mask_builder=plain, topk=2)
     assert torch.equal(a_top, b_top) and torch.equal(a_g, b_g)
+
+
+@pytest.mark.parametrize("side,entry", [("target", "d3d_accept_fused"), ("draft", "d3d_topk_rows")])
+def test_failed_launch_on_either_stream_raises(side, entry):
+    """A launch that fails on the verify (target) or the draft stream -- the
+    library call reports a HIP error on the third call -- surfaces from
+    generate as RuntimeError naming the side, after both streams drain
+    (the in-process form of serving/target_process.py:82-96)."""
+    from d3d_amd import _lib
+    eng = _engine(29, use_graphs=False)
+    lib = _lib.load()
+    real = getattr(lib, entry)
+    calls = {"n": 0}
+
+    def failing(*args):
+        calls["n"] += 1
+        return 98 if calls["n"] == 3 else real(*args)  # 98: hipErrorInvalidDeviceFunction
+
+    setattr(lib, entry, failing)
+    try:
+        prompts = torch.randint(0, 999, (2, 20), generator=torch.Generator().manual_seed(9)).tolist()
+        with pytest.raises(RuntimeError, match=f"{side} step failed"):
+            eng.generate(prompts, 2, max_new_tokens=10, ignore_eos=True)
+    finally:
+        setattr(lib, entry, real)
+    torch.cuda.synchronize()
+    # The library is usable again afterwards.
+    ok = _engine(29, use_graphs=False).generate([[1, 2, 3]], 1, max_new_tokens=4, ignore_eos=True)
+    assert len(ok["outputs"][0]["tokens"]) == 4
