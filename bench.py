@@ -16,8 +16,10 @@ exactly one token and K tokens are K steps.  steps/s counts decode
 iterations over their wall time (admission and prefill excluded).
 
 ``rooflines`` lists the kernels each configuration names, each timed with
-HIP events on its launch stream over repeated calls with inputs resident in
-HBM; ``frac`` = algorithmic bytes / call duration / 8 TB/s:
+HIP events on its launch stream over repeated calls; every call reads the
+next of several input sets totalling over 640 MB, so its inputs come from
+HBM rather than the 256 MB memory-side cache; ``frac`` = algorithmic bytes /
+call duration / 8 TB/s:
 
 * config 0: fused acceptance, batch 1, 16 target + 15 draft fp32 rows over
   V = 151,936 at T = 1 (18,840,064 B) and greedy (16 rows, 9,723,904 B);
@@ -198,6 +200,28 @@ def time_calls(fn, steps: int, warmup: int, dev) -> float:
     return start.elapsed_time(end) / steps
 
 
+# MI355X has a 256 MB memory-side cache (MALL) in front of HBM.  A kernel
+# that re-reads one input set finds part of it there, so each roofline call
+# takes the next of several input sets whose total exceeds 640 MB: every
+# call's inputs come from HBM.
+COLD_BYTES = 640 << 20
+
+
+class Rotating:
+    """Cycles through ``n`` independent instances of a pre-bound call."""
+
+    def __init__(self, make, set_bytes: int, max_sets: int = 40):
+        n = max(2, min(max_sets, -(-COLD_BYTES // max(set_bytes, 1))))
+        self.calls = [make(i) for i in range(n)]
+        self.i = 0
+        self.bytes = self.calls[0].bytes
+        self.flops = getattr(self.calls[0], "flops", None)
+
+    def __call__(self):
+        self.calls[self.i]()
+        self.i = (self.i + 1) % len(self.calls)
+
+
 def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None):
     gbps = nbytes / (ms * 1e-3) / 1e9
     out = {"config": config, "kernel": kernel, "bound": "hbm", "algorithmic_bytes": int(nbytes),
@@ -209,37 +233,38 @@ def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None):
 
 
 def kernel_rooflines(dev, calls: int):
+    """Each configuration's kernels with cold (HBM-resident) inputs."""
     from d3d_amd import workloads
     warm = max(calls // 10, 3)
     out = []
-    acc = AcceptStep(workloads.accept_inputs(1234, B=1, K=15, device="cuda"), 1.0, dev)
-    out.append(_roof(0, "fused acceptance, batch 1, T=1", acc.bytes, time_calls(acc, calls, warm, dev), 0.70,
-                     TRAFFIC["c0_accept_t1"]))
-    del acc
-    g = AcceptStep(workloads.accept_inputs(1234, B=1, K=15, temperature=0.0, device="cuda"), 0.0, dev)
-    out.append(_roof(0, "fused acceptance, batch 1, greedy", g.bytes, time_calls(g, calls, warm, dev), 0.70))
-    del g
-    v1 = AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234, num_pages=256)
-    out.append(_roof(1, "block-verify attention, batch 1, prefix 2048", v1.bytes, time_calls(v1, calls, warm, dev),
-                     0.60, TRAFFIC["c1_verify_attn"], v1.flops))
-    del v1
+
+    def acc(B, T):
+        return lambda i: AcceptStep(workloads.accept_inputs(1234 + i, B=B, K=15, temperature=T, device="cuda"),
+                                    T, dev)
+
+    def run(make, set_bytes):
+        r = Rotating(make, set_bytes)
+        ms = time_calls(r, calls, warm, dev)
+        return r, ms
+
+    r, ms = run(acc(1, 1.0), 31 * 151936 * 4)
+    out.append(_roof(0, "fused acceptance, batch 1, T=1", r.bytes, ms, 0.70, TRAFFIC["c0_accept_t1"]))
+    r, ms = run(acc(1, 0.0), 31 * 151936 * 4)
+    out.append(_roof(0, "fused acceptance, batch 1, greedy", r.bytes, ms, 0.70))
+    r, ms = run(lambda i: AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234 + i, num_pages=256), 8_716_804)
+    out.append(_roof(1, "block-verify attention, batch 1, prefix 2048", r.bytes, ms, 0.60,
+                     TRAFFIC["c1_verify_attn"], r.flops))
     lens8 = [c + 16 for c in workloads.concurrent_context_lens(2024, B=8)]
-    v8 = AttnStep(lens8, 16, 32, 8, 16, True, dev, seed=2024)
-    out.append(_roof(2, f"block-verify attention, batch 8, contexts {lens8}", v8.bytes,
-                     time_calls(v8, calls, warm, dev), 0.60, TRAFFIC["c2_verify_attn"], v8.flops))
-    del v8
-    b8 = AcceptStep(workloads.accept_inputs(1234, B=8, K=15, device="cuda"), 1.0, dev)
-    out.append(_roof(2, "fused acceptance, batch 8, T=1", b8.bytes, time_calls(b8, calls, warm, dev), 0.70,
-                     TRAFFIC["c2_accept_b8"]))
-    del b8
-    d4 = AttnStep([1024 + 16] * 4, 16, 16, 8, 16, False, dev, seed=77)
-    out.append(_roof(3, "draft block attention, batch 4, prefix 1024", d4.bytes, time_calls(d4, calls, warm, dev),
-                     0.60, None, d4.flops))
-    del d4
-    cf = ConfStep(4, 16, 151936, 4, dev, seed=5)
-    out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", cf.bytes, time_calls(cf, calls, warm, dev),
-                     0.70))
-    del cf
+    r, ms = run(lambda i: AttnStep(lens8, 16, 32, 8, 16, True, dev, seed=2024 + i), 126_471_608)
+    out.append(_roof(2, f"block-verify attention, batch 8, contexts {lens8}", r.bytes, ms, 0.60,
+                     TRAFFIC["c2_verify_attn"], r.flops))
+    r, ms = run(acc(8, 1.0), 248 * 151936 * 4)
+    out.append(_roof(2, "fused acceptance, batch 8, T=1", r.bytes, ms, 0.70, TRAFFIC["c2_accept_b8"]))
+    r, ms = run(lambda i: AttnStep([1024 + 16] * 4, 16, 16, 8, 16, False, dev, seed=77 + i), 17_564_688)
+    out.append(_roof(3, "draft block attention, batch 4, prefix 1024", r.bytes, ms, 0.60, None, r.flops))
+    r, ms = run(lambda i: ConfStep(4, 16, 151936, 4, dev, seed=5 + i), 19_447_808)
+    out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", r.bytes, ms, 0.70))
+    del r
     torch.cuda.empty_cache()
     return out
 

@@ -23,6 +23,7 @@ D3D_CONF_MAX_SOFTMAX = 0
 D3D_CONF_ONE_HOT = 1
 D3D_TOKEN_EMPTY_DISTRIBUTION = -1
 D3D_TOKEN_BAD_DRAFT = -2
+D3D_TOKEN_TIMEOUT = -3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

@@ -1,27 +1,37 @@
 // Fused speculative acceptance for gfx950.
 //
-// Three stream-ordered phases, no atomics and no cross-workgroup waits:
+// Two stream-ordered launches:
 //
-//   1. stats     grid (C, rows, B).  Workgroup (c, r, b) streams chunk c of
-//                row r of request b once (target rows 0..K, then draft rows
-//                0..K-1; greedy mode reads target rows only) and reduces it to
-//                (max z, sum exp(z - max z), max x, argmax) with z = x / T, or
-//                to a plain sum for probability inputs.
-//   2. decide    grid (C, B).  Every workgroup of request b merges the chunk
-//                statistics of all rows in one fixed order (so all of them
-//                reach the same bits), evaluates u_i <= min(1, p_i / max(q_i,
-//                1e-12)) at every position and finds the first reject.
-//                Workgroup 0 writes the outputs; in stochastic modes every
-//                workgroup then reduces chunk c of the selected row pair
-//                (residual max(p - q, 0), and p) to chunk sums.
-//   3. resample  grid (B), stochastic modes only.  Locates the chunk in which
-//                the inverse CDF crosses u * W and scans it entry by entry.
+//   1. stats   grid (C, rows, B).  Workgroup (c, r, b) streams chunk c of row
+//              r of request b once (target rows 0..K, then draft rows 0..K-1;
+//              greedy mode and sparse proposals read target rows only) and
+//              reduces it to (max z, sum exp(z - max z), max x, argmax) with
+//              z = x / T, or to a plain sum for probability inputs.  One chunk
+//              per workgroup and no cross-workgroup traffic: the HBM-bound
+//              pass runs at the rate of a plain streaming read.
+//   2. finish  grid B * C (greedy: B).  Every workgroup of request b merges
+//              the request's chunk records (a few KiB, from L2) into row
+//              statistics, evaluates u_i <= min(1, p_i / max(q_i, 1e-12)) at
+//              every position and finds the first reject n, each computing
+//              the same bits; the request's last workgroup writes the
+//              decision outputs.  Workgroup q then reduces part q (4096
+//              entries) of the selected row pair to the sums of the residual
+//              max(p - q, 0) and of p, publishes them as a tagged record and
+//              collects every other part's record (one wave, polling).  Each
+//              workgroup then runs the same part-level inverse CDF; the one
+//              whose part holds the crossing of u * W scans its entries, still
+//              in registers, and writes the token.
 //
-// The phases replace per-workgroup completion counters: on MI355X a
-// device-scope release per workgroup (L2 write-back across XCDs) and
-// same-address atomics serialise, and cost far more than two extra launches
-// (folding phase 3 into phase 2 with a last-workgroup counter measured
-// 17 -> 22 us at one request and 43 -> 60 us at eight).
+// The part records are the only cross-workgroup hand-off: each is written
+// as two agent-scope atomic 8-byte stores, every word carrying a nonzero tag
+// next to its value, and polled with agent-scope atomic loads until every
+// tag is set (the stats launch of the same call clears them, so the
+// workspace needs no initial contents).  No fence, counter or L2 write-back
+// sits on the path.  A workgroup waits only for the other workgroups of its
+// own request, and only after publishing its own record; workgroups are
+// dispatched in index order, so the lowest unfinished request always has
+// all of its workgroups dispatched, its waits end, and so on by induction.  Each wait is bounded
+// regardless: on expiry the token stays D3D_TOKEN_TIMEOUT.
 //
 // Reference semantics (D3D repository):
 //   single/eval_sync.py:287-305           temperature softmax / greedy one-hot
@@ -32,11 +42,10 @@
 //
 // Sparse proposals (single/speculative_sampling.py:79-143): the draft side is
 // a support of S (id, probability) pairs per position instead of a dense row.
-// Phase 1 then reads target rows only; phase 2 computes q at the draft token
-// as the normalised support mass on that id, and the residual of the reject
-// row subtracts the normalised support from p entry by entry, in support
-// order (scatter_add), before the clamp at zero.  Ids outside [0, V) carry
-// no mass.
+// Phase 1 then reads target rows only (and computes the support mass and q
+// at each draft token); the residual of the reject row subtracts the
+// normalised support from p entry by entry, in support order (scatter_add),
+// before the clamp at zero.  Ids outside [0, V) carry no mass.
 //
 // Every reduction runs in one fixed order for a given (V, dtype), so outputs
 // are deterministic.  The stochastic draw replaces torch.multinomial with an
@@ -56,29 +65,23 @@ namespace accept {
 using namespace rows;
 
 constexpr int kMaxK = 127;       // K+1 target rows + K draft rows <= 255
-// Phases 2 and 3 are latency-bound, so their chunks hold nv2 16-byte vectors
-// per thread (nv2 in 1..kMaxNv2), chosen per launch: few requests get fine
-// chunks (more workgroups, shorter per-thread chains), many requests get
-// coarse ones (fewer redundant row merges).
-constexpr int kMaxNv2 = 4;
-constexpr int kMaxS = 1024;  // sparse support entries per position
+constexpr int kMaxS = 1024;      // sparse support entries per position
+constexpr int kPart = 4096;      // residual part: entries per workgroup
+constexpr int kRun = kPart / NT; // contiguous entries per thread in a part
+constexpr int kMaxParts = kMaxStatLds;  // V <= kMaxStatLds * kChunk
+static_assert(kPart == kChunk, "part q is cleared by the stats workgroup of chunk q");
+// Polls of a part record before a waiting workgroup gives up (with
+// s_sleep 2 between polls, well over 100 ms).
+constexpr int kSpinLimit = 1 << 20;
 
-struct Decision {
-    int n;  // first rejected position (K when all accepted)
-    int flags;
-    float Mt, St, Mq, Sq;  // row statistics of the selected target/draft rows
-                           // (sparse proposals: Sq = support mass of the reject row)
-    int pad0, pad1;
+// Part record: two 8-byte words, each a float and a tag that is nonzero
+// once written (tag = last positive index + 2).
+struct PartRec {
+    float r;  // sum of residual weights max(p - q, 0) over the part
+    int tr;   // last index with positive residual + 2
+    float p;  // sum of target probabilities over the part
+    int tp;   // last index with positive probability + 2
 };
-
-struct ResStat {
-    float r;     // sum of residual weights over the chunk
-    float p;     // sum of target probabilities over the chunk
-    int last_r;  // last index with positive residual (-1 if none)
-    int last_p;  // last index with positive probability (-1 if none)
-};
-
-enum : int { kFlagInvalid = 1 };
 
 struct Params {
     const void* target;
@@ -87,15 +90,16 @@ struct Params {
     const float* uniforms;
     const float* resample_u;
     float T;
+    int B;
     int K;
     int V;
-    int C;   // phase-1 chunks per row
-    int C2;  // phase-2/3 sub-chunks per row (NT 16-byte vectors each)
-    int nv2; // sub-chunks per phase-2 workgroup
+    int C;    // chunks (= parts) per row
+    int Rm;   // rows merged per request: K + 1 (greedy, sparse) or 2K + 1
     RowStat* stats;  // [B][R][C], R = 2K+1 (target rows 0..K, draft rows K+1..2K)
-    Decision* dec;   // [B]
-    ResStat* rstats; // [B][C]
-    float* xtok;     // [B][R]: value of row r at its draft token (rows != K)
+    float* xtok;     // [B][R]: value of row r at its draft token (rows != K);
+                     // sparse proposals: q at draft token i in slot K+1+i
+    float* zsp;      // [B][K]: sparse support mass max(sum_s q_s, 1e-12)
+    PartRec* parts;  // [B][C], cleared by the stats launch
     const int64_t* q_ids;  // sparse proposals [B][K][S], else null
     const float* q_probs;  // [B][K][S]
     int S;
@@ -105,6 +109,32 @@ struct Params {
     uint8_t* all_accepted;
     int64_t* posterior;
 };
+
+// 8-byte agent-scope atomic store / load: coherent across XCDs without an
+// L2 write-back.
+__device__ __forceinline__ void store_word(void* dst, float v, int tag) {
+    const uint64_t w = (uint64_t)__float_as_uint(v) | ((uint64_t)(uint32_t)tag << 32);
+    __hip_atomic_store(static_cast<uint64_t*>(dst), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t load_word(const void* src) {
+    return __hip_atomic_load(static_cast<const uint64_t*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sparse support mass Z = max(sum_s q_s, 1e-12) of position i and the
+// normalised mass on token tok (sum over matching ids of q_s / Z), one wave
+// per call.
+__device__ __forceinline__ void sparse_q_at(const Params& P, int b, int i, int64_t tok, float& Z, float& qt) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t row = ((size_t)b * P.K + i) * P.S;
+    float z = 0.f;
+    for (int s = lane; s < P.S; s += kWave) z += P.q_probs[row + s];
+    Z = fmaxf(wave_sum(z), 1e-12f);
+    float m = 0.f;
+    for (int s = lane; s < P.S; s += kWave)
+        if (P.q_ids[row + s] == tok) m += P.q_probs[row + s] / Z;
+    qt = wave_sum(m);
+}
 
 // ---------------------------------------------------------------- phase 1
 template <int DT, bool VEC, Mode M>
@@ -132,24 +162,27 @@ __global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
         // The workgroup whose chunk holds the token records its value once.
         if (M != kGreedy && tok >= (int64_t)c * kChunk && tok < (int64_t)(c + 1) * kChunk && tok < V)
             P.xtok[(size_t)b * R + r] = load_one<DT>(row, (int)tok);
+        // Part record c of this request starts untagged, and the output
+        // token at the timeout sentinel, for the finish launch (stream
+        // order makes the stores visible to it).
+        if (M != kGreedy && r == 0) {
+            P.parts[(size_t)b * C + c] = PartRec{0.f, 0, 0.f, 0};
+            if (c == 0) P.out_token[b] = D3D_TOKEN_TIMEOUT;
+        }
+    }
+    // Sparse proposals: chunk 0 of target row i also reduces position i's
+    // support (one wave): its mass and q at draft token i.
+    if (M != kGreedy && P.S > 0 && c == 0 && r < K && threadIdx.x < kWave) {
+        float Z, qt;
+        sparse_q_at(P, b, r, P.tokens[(size_t)b * K + r], Z, qt);
+        if (threadIdx.x == 0) {
+            P.xtok[(size_t)b * R + K + 1 + r] = qt;
+            P.zsp[(size_t)b * K + r] = Z;
+        }
     }
 }
 
 // ---------------------------------------------------------------- sparse
-// Support mass Z = max(sum_s q_s, 1e-12) of position i and the normalised
-// mass on token tok (sum over matching ids of q_s / Z), one wave per call.
-__device__ __forceinline__ void sparse_q_at(const Params& P, int b, int i, int64_t tok, float& Z, float& qt) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const size_t row = ((size_t)b * P.K + i) * P.S;
-    float z = 0.f;
-    for (int s = lane; s < P.S; s += kWave) z += P.q_probs[row + s];
-    Z = fmaxf(wave_sum(z), 1e-12f);
-    float m = 0.f;
-    for (int s = lane; s < P.S; s += kWave)
-        if (P.q_ids[row + s] == tok) m += P.q_probs[row + s] / Z;
-    qt = wave_sum(m);
-}
-
 // Residual weights of a sparse proposal over entries [lo, lo + span): buf
 // holds p at local index e - lo on entry and p - sum(q_s / Z) (support
 // order, unclamped) at every support id on exit.  Block-wide; every thread
@@ -178,66 +211,39 @@ __device__ __forceinline__ void sparse_subtract(const Params& P, int b, int n, f
 }
 
 // ---------------------------------------------------------------- phase 2
-// Row statistics of request b: sM/sS per row (target rows 0..K, draft rows
-// K+1..2K) and sArg for target rows.
-template <Mode M, bool SP>
-__device__ __forceinline__ void merge_rows(const Params& P, int b, float* sM, float* sS, int* sArg,
-                                           RowStat* lds) {
-    const int K = P.K, C = P.C, R = 2 * K + 1;
-    merge_row_stats<M>(P.stats + (size_t)b * R * C, (M == kGreedy || SP) ? K + 1 : R, C, K + 1, sM, sS, sArg,
-                       lds);
-}
+// The decision of request b, computed with the same bits by each of its
+// workgroups.
+struct Decision {
+    int n;     // first rejected position (K when all accepted)
+    bool bad;  // a draft token outside [0, V)
+    float Mt, It;  // selected target row: max z and 1 / normaliser
+    float Mq, Iq;  // selected draft row (dense proposals)
+    float Zq;      // support mass of the selected position (sparse proposals)
+};
 
-// One descending butterfly step of the residual chunk sums (sub-chunks
-// j < nv2): sums of r and p, last positive index of each.
-template <int O>
-__device__ __forceinline__ void res_step(float (&rs)[kMaxNv2], float (&ps)[kMaxNv2], int (&lr)[kMaxNv2],
-                                         int (&lp)[kMaxNv2], int nv2) {
-#pragma unroll
-    for (int j = 0; j < kMaxNv2; ++j) {
-        if (j >= nv2) break;
-        rs[j] += xor_desc<O>(rs[j]);
-        ps[j] += xor_desc<O>(ps[j]);
-        lr[j] = max(lr[j], xor_desc<O>(lr[j]));
-        lp[j] = max(lp[j], xor_desc<O>(lp[j]));
-    }
-}
-
-template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
-__device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowStat* lds, float* sM, float* sS,
-                                            int* sArg, uint64_t* s_bits, float* rf, int* ri) {
-    __shared__ float sQt[SP ? kMaxK : 1], sZ[SP ? kMaxK : 1];
-    constexpr int E = Vec<DT>::E;
-    const int K = P.K, V = P.V;
+// Merges the request's chunk records, evaluates the accept test at every
+// position and finds the first reject; the writer also stores the decision
+// outputs (and, in greedy mode or on a bad draft, the output token).
+template <int DT, Mode M, bool UNIT_T, bool SP>
+__device__ __forceinline__ Decision decide(const Params& P, int b, bool writer) {
+    __shared__ float sM[2 * kMaxK + 1], sS[2 * kMaxK + 1];
+    __shared__ int sArg[kMaxK + 1];
+    __shared__ RowStat lds[kMaxStatLds];
+    __shared__ uint64_t s_bits[4];
+    const int K = P.K, V = P.V, R = 2 * K + 1;
     const int tid = threadIdx.x;
-
-    // Independent loads first: tokens, uniforms and token values.
+    // Per-position inputs first: their loads overlap the record merge.
     int64_t tok = 0;
     float u = 0.f, xt = 0.f, xq = 0.f;
     if (tid < K) {
         tok = P.tokens[(size_t)b * K + tid];
         if (M != kGreedy) {
             u = P.uniforms[(size_t)b * K + tid];
-            xt = P.xtok[(size_t)b * (2 * K + 1) + tid];
-            if (!SP) xq = P.xtok[(size_t)b * (2 * K + 1) + K + 1 + tid];
+            xt = P.xtok[(size_t)b * R + tid];
+            xq = P.xtok[(size_t)b * R + K + 1 + tid];  // draft row value, or sparse q
         }
     }
-    if constexpr (SP) {
-        // q at the draft token of every position, one wave per position.
-        for (int i = tid / kWave; i < K; i += NT / kWave) {
-            float Z, qt;
-            sparse_q_at(P, b, i, P.tokens[(size_t)b * K + i], Z, qt);
-            if ((tid & (kWave - 1)) == 0) {
-                sZ[i] = Z;
-                sQt[i] = qt;
-            }
-        }
-    }
-    merge_rows<M, SP>(P, b, sM, sS, sArg, lds);
-    if constexpr (SP) __syncthreads();
-
-    // Per-position decisions, then the first reject and the bad-token flag
-    // from wave ballots (positions 0..K-1 live in waves 0 and 1).
+    merge_row_stats<M>(P.stats + (size_t)b * R * P.C, P.Rm, P.C, K + 1, sM, sS, sArg, lds);
     bool acc = false, badp = false;
     if (tid < K) {
         badp = tok < 0 || tok >= V;
@@ -246,8 +252,7 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         } else {
             if (!badp) {
                 const float pt = prob_of<M, UNIT_T>(xt, sM[tid], inv_sum<M>(sS[tid]), P.T);
-                const float qt = SP ? sQt[tid]
-                                    : prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
+                const float qt = SP ? xq : prob_of<M, UNIT_T>(xq, sM[K + 1 + tid], inv_sum<M>(sS[K + 1 + tid]), P.T);
                 const float a = fminf(1.0f, pt / fmaxf(qt, 1e-12f));
                 acc = u <= a;
             }
@@ -263,380 +268,336 @@ __device__ __forceinline__ void decide_body(const Params& P, int c, int b, RowSt
         }
     }
     __syncthreads();
-    const int n = s_bits[0] ? __builtin_ctzll(s_bits[0]) : (s_bits[1] ? 64 + __builtin_ctzll(s_bits[1]) : K);
-    const bool bad = (s_bits[2] | s_bits[3]) != 0;
-    if (c == 0) {
+    Decision d;
+    d.n = s_bits[0] ? __builtin_ctzll(s_bits[0]) : (s_bits[1] ? 64 + __builtin_ctzll(s_bits[1]) : K);
+    d.bad = (s_bits[2] | s_bits[3]) != 0;
+    const int n = d.n;
+    if (writer) {
         for (int p = tid; p < K; p += NT) P.mask[(size_t)b * K + p] = acc;
         if (P.posterior)
             for (int r = tid; r <= K; r += NT) P.posterior[(size_t)b * (K + 1) + r] = sArg[r];
         if (tid == 0) {
-            P.accepted[b] = bad ? 0 : n;
-            P.all_accepted[b] = !bad && n == K;
-            if (M == kGreedy || bad)
-                P.out_token[b] = bad ? (int64_t)D3D_TOKEN_BAD_DRAFT : (int64_t)sArg[n];
-            if (M != kGreedy) {
-                Decision d;
-                d.n = n;
-                d.flags = bad ? kFlagInvalid : 0;
-                d.Mt = sM[n];
-                d.St = sS[n];
-                d.Mq = (n < K && !SP) ? sM[K + 1 + n] : 0.f;
-                d.Sq = n < K ? (SP ? sZ[n] : sS[K + 1 + n]) : 0.f;
-                d.pad0 = d.pad1 = 0;
-                P.dec[b] = d;
-            }
+            P.accepted[b] = d.bad ? 0 : n;
+            P.all_accepted[b] = !d.bad && n == K;
+            if (M == kGreedy || d.bad)
+                P.out_token[b] = d.bad ? (int64_t)D3D_TOKEN_BAD_DRAFT : (int64_t)sArg[n];
         }
     }
-    if constexpr (M != kGreedy) {
-        if (bad) return;
-        // Chunk sums of the selected row pair (reject row, or bonus row).
-        const bool res = n < K;
-        const void* trow = row_ptr<DT>(P.target, (size_t)b * (K + 1) + n, V);
-        const bool dres = res && !SP;  // dense draft row to read
-        const void* drow = dres ? row_ptr<DT>(P.draft, (size_t)b * K + n, V) : nullptr;
-        const float Mt = sM[n], It = inv_sum<M>(sS[n]);
-        const float Mq = dres ? sM[K + 1 + n] : 0.f, Iq = dres ? inv_sum<M>(sS[K + 1 + n]) : 0.f;
-        // Workgroup c covers sub-chunks c*nv2 .. c*nv2+nv2-1; sub-chunk j is
-        // vector j of every thread (NT*E consecutive entries) and gets its own
-        // record, so phase 3 always scans one vector per thread.
-        constexpr int LM = kMaxNv2 * E;
-        const int nv2 = P.nv2;
-        const int first = c * (NT * E * nv2) + tid * E;
-        float xt[LM], xq[LM];
-        load_tile_n<DT, VEC, LM>(trow, V, first, NT * E, nv2, fill_value<M>(), xt);
-        if (dres) load_tile_n<DT, VEC, LM>(drow, V, first, NT * E, nv2, fill_value<M>(), xq);
-        if constexpr (SP) {
-            // xq <- p - q (unclamped) through the workgroup's LDS copy of p.
-            __shared__ float buf[NT * kMaxNv2 * E];
-            __shared__ int s_id[kMaxS];
-            __shared__ float s_q[kMaxS];
-            const int lo = c * (NT * E * nv2);
-#pragma unroll
-            for (int j = 0; j < kMaxNv2; ++j)
-#pragma unroll
-                for (int k = 0; k < E; ++k)
-                    if (j < nv2) buf[j * NT * E + tid * E + k] = prob_of<M, UNIT_T>(xt[j * E + k], Mt, It, P.T);
-            if (res) sparse_subtract(P, b, n, sZ[n], lo, NT * E * nv2, buf, s_id, s_q);
-#pragma unroll
-            for (int j = 0; j < kMaxNv2; ++j)
-#pragma unroll
-                for (int k = 0; k < E; ++k)
-                    if (j < nv2) xq[j * E + k] = buf[j * NT * E + tid * E + k];
+    d.Mt = sM[n];
+    d.It = inv_sum<M>(sS[n]);
+    d.Mq = 0.f;
+    d.Iq = 0.f;
+    d.Zq = 1.f;
+    if (M != kGreedy && n < K) {
+        if (SP) {
+            d.Zq = P.zsp[(size_t)b * K + n];
+        } else {
+            d.Mq = sM[K + 1 + n];
+            d.Iq = inv_sum<M>(sS[K + 1 + n]);
         }
-        float rs[kMaxNv2], ps[kMaxNv2];
-        int lr[kMaxNv2], lp[kMaxNv2];
+    }
+    return d;
+}
+
+// Entries e0 .. e0 + kRun - 1 of a row (fill past V).
+template <int DT, bool VEC, Mode M>
+__device__ __forceinline__ void load_run(const void* row, int V, int e0, float (&x)[kRun]) {
+    constexpr int E = Vec<DT>::E;
+    if (VEC && e0 + kRun <= V) {
 #pragma unroll
-        for (int j = 0; j < kMaxNv2; ++j) {
-            rs[j] = ps[j] = 0.f;
-            lr[j] = lp[j] = -1;
-            if (j >= nv2) continue;
+        for (int j = 0; j < kRun / E; ++j) {
+            if constexpr (DT == kF32) {
+                const f32x4 v = reinterpret_cast<const f32x4*>(static_cast<const float*>(row) + e0)[j];
+                x[j * 4 + 0] = v.x;
+                x[j * 4 + 1] = v.y;
+                x[j * 4 + 2] = v.z;
+                x[j * 4 + 3] = v.w;
+            } else {
+                const u32x4 v = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(row) + e0)[j];
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int k = 0; k < E; ++k) {
-                const int l = j * E + k;
-                const int e = first + j * NT * E + k;
-                const float p = prob_of<M, UNIT_T>(xt[l], Mt, It, P.T);
-                ps[j] += p;
-                if (p > 0.f) lp[j] = e;
-                if (res) {
-                    const float r = SP ? fmaxf(xq[l], 0.f) : fmaxf(p - prob_of<M, UNIT_T>(xq[l], Mq, Iq, P.T), 0.f);
-                    rs[j] += r;
-                    if (r > 0.f) lr[j] = e;
+                for (int h = 0; h < 4; ++h) {
+                    x[j * 8 + 2 * h] = bf16_bits_to_f32(w[h] & 0xffffu);
+                    x[j * 8 + 2 * h + 1] = bf16_bits_to_f32(w[h] >> 16);
                 }
             }
         }
-        // One combined workgroup reduction for the nv2 sub-chunks.
-        res_step<32>(rs, ps, lr, lp, nv2);
-        res_step<16>(rs, ps, lr, lp, nv2);
-        res_step<8>(rs, ps, lr, lp, nv2);
-        res_step<4>(rs, ps, lr, lp, nv2);
-        res_step<2>(rs, ps, lr, lp, nv2);
-        res_step<1>(rs, ps, lr, lp, nv2);
-        __shared__ ResStat s_red[NT / kWave][kMaxNv2];
-        const int lane = tid & (kWave - 1), wv = tid / kWave;
-        if (lane == 0)
+    } else {
 #pragma unroll
-            for (int j = 0; j < kMaxNv2; ++j) s_red[wv][j] = ResStat{rs[j], ps[j], lr[j], lp[j]};
-        __syncthreads();
-        if (tid < nv2 && c * nv2 + tid < P.C2) {
-            ResStat st = s_red[0][tid];
-            for (int w = 1; w < NT / kWave; ++w) {
-                const ResStat t = s_red[w][tid];
-                st.r += t.r;
-                st.p += t.p;
-                st.last_r = max(st.last_r, t.last_r);
-                st.last_p = max(st.last_p, t.last_p);
-            }
-            P.rstats[(size_t)b * P.C2 + c * nv2 + tid] = st;
+        for (int k = 0; k < kRun; ++k) x[k] = e0 + k < V ? load_one<DT>(row, e0 + k) : fill_value<M>();
+    }
+}
+
+// Weights of this thread's run of part q: wr = the residual max(p - q, 0)
+// (zero when every position was accepted), wp = p.  Sparse proposals
+// subtract the support through an LDS copy of the part.  Block-wide.
+template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
+__device__ __forceinline__ void part_weights(const Params& P, int b, const Decision& d, int q, float (&wr)[kRun],
+                                             float (&wp)[kRun]) {
+    const int K = P.K, V = P.V;
+    const bool res = d.n < K;
+    const int e0 = q * kPart + (int)threadIdx.x * kRun;
+    float xt[kRun];
+    load_run<DT, VEC, M>(row_ptr<DT>(P.target, (size_t)b * (K + 1) + d.n, V), V, e0, xt);
+#pragma unroll
+    for (int k = 0; k < kRun; ++k) wp[k] = prob_of<M, UNIT_T>(xt[k], d.Mt, d.It, P.T);
+    if constexpr (SP) {
+        __shared__ float buf[kPart];
+        __shared__ int s_id[kMaxS];
+        __shared__ float s_q[kMaxS];
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) buf[threadIdx.x * kRun + k] = wp[k];
+        if (res) sparse_subtract(P, b, d.n, d.Zq, q * kPart, kPart, buf, s_id, s_q);
+        else __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) wr[k] = res ? fmaxf(buf[threadIdx.x * kRun + k], 0.f) : 0.f;
+        __syncthreads();  // buf is reused by the next call
+    } else {
+        if (res) {
+            float xq[kRun];
+            load_run<DT, VEC, M>(row_ptr<DT>(P.draft, (size_t)b * K + d.n, V), V, e0, xq);
+#pragma unroll
+            for (int k = 0; k < kRun; ++k) wr[k] = fmaxf(wp[k] - prob_of<M, UNIT_T>(xq[k], d.Mq, d.Iq, P.T), 0.f);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kRun; ++k) wr[k] = 0.f;
         }
     }
 }
 
-template <int DT, bool VEC, Mode M, bool SP>
-__global__ __launch_bounds__(NT) void accept_decide_kernel(Params P) {
-    __shared__ RowStat lds[kMaxStatLds];
-    __shared__ float sM[2 * kMaxK + 2], sS[2 * kMaxK + 2];
-    __shared__ int sArg[kMaxK + 1];
-    __shared__ uint64_t s_bits[4];
-    __shared__ float rf[NT / kWave];
-    __shared__ int ri[NT / kWave];
-    if (P.T == 1.0f)
-        decide_body<DT, VEC, M, true, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, s_bits, rf, ri);
-    else
-        decide_body<DT, VEC, M, false, SP>(P, blockIdx.x, blockIdx.y, lds, sM, sS, sArg, s_bits, rf, ri);
+// Sums of the weights over the workgroup's part, their last positive
+// indices, and each thread's exclusive prefix of its run sums within the
+// part (thread order), for the residual (r) and target (p) weights: wave
+// scans on the VALU, one barrier.  The part sums are the totals of the same
+// scan, so a crossing located by the part sums is met again by the entry
+// scan of the part.
+struct PartSums {
+    float r, p;
+    int lr, lp;
+};
+
+__device__ __forceinline__ PartSums block_part_scan(float tr, float tp, int lr, int lp, float4* s4, float& xr,
+                                                    float& xp) {
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+    const float ir = wave_incl_scan(tr, lane), ip = wave_incl_scan(tp, lane);
+    const float er = up_f<1>(ir), ep = up_f<1>(ip);  // lane - 1's inclusive value
+    lr = wave_max_int(lr);
+    lp = wave_max_int(lp);
+    if (lane == kWave - 1) s4[wv] = make_float4(ir, ip, __int_as_float(lr), __int_as_float(lp));
+    __syncthreads();
+    PartSums o{0.f, 0.f, -1, -1};
+    float offr = 0.f, offp = 0.f;
+#pragma unroll
+    for (int k = 0; k < NT / kWave; ++k) {
+        const float4 t = s4[k];
+        if (k == wv) {
+            offr = o.r;
+            offp = o.p;
+        }
+        o.r += t.x;
+        o.p += t.y;
+        o.lr = max(o.lr, __float_as_int(t.z));
+        o.lp = max(o.lp, __float_as_int(t.w));
+    }
+    xr = lane ? offr + er : offr;
+    xp = lane ? offp + ep : offp;
+    return o;
 }
 
-// ---------------------------------------------------------------- phase 3
-template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
-__device__ __forceinline__ void resample_body(const Params& P, int b, float* s_wave, float* s_f, int* s_i,
-                                              int* ri) {
-    constexpr int E = Vec<DT>::E;
-    const int K = P.K, V = P.V, C = P.C2;
-    const int tid = threadIdx.x;
-    // All independent loads are issued before the first use.
-    const Decision d = P.dec[b];
-    const float v = P.resample_u[b];
-    ResStat mine0;  // this thread's chunk record of the first pass, reused below
-    mine0.r = mine0.p = 0.f;
-    mine0.last_r = mine0.last_p = -1;
-    if (tid < C) mine0 = P.rstats[(size_t)b * C + tid];
-    if (d.flags & kFlagInvalid) return;
-    const bool res = d.n < K;
-    const float It = inv_sum<M>(d.St), Iq = (res && !SP) ? inv_sum<M>(d.Sq) : 0.f;
+// Lowest `found` and highest `last` over the workgroup, one barrier.
+__device__ __forceinline__ void block_min_max(int& found, int& last, int2* s2) {
+    found = wave_min_int(found);
+    last = wave_max_int(last);
+    if ((threadIdx.x & (kWave - 1)) == 0) s2[threadIdx.x / kWave] = make_int2(found, last);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NT / kWave; ++k) {
+        found = min(found, s2[k].x);
+        last = max(last, s2[k].y);
+    }
+}
 
-    // Chunk-level inverse CDF: inclusive scan of chunk sums in chunk order,
-    // the crossing chunk is the first whose inclusive sum exceeds v * W.
-    // The weights are the residual unless its mass is <= 1e-12.
+// What wave 0 of every part workgroup derives from all part records.
+struct Crossing {
+    int late;   // a record did not arrive within the bound
+    int cs;     // part where the inverse CDF crosses u * W (INT_MAX: none)
+    int use_r;  // residual weights (else p)
+    int last;   // last positive index over the row (fallback token)
+    float W, target, base;  // total, u * W, weight of the parts before cs
+};
+
+// Wave 0: collects every part's sums (its own from registers, the others
+// by polling their tagged records), then the part-level inverse CDF in
+// part order.  Every workgroup of the request computes the same bits.
+__device__ __forceinline__ Crossing find_crossing(const Params& P, int b, int q, const Decision& d,
+                                                  const PartSums& own, float* s_r, float* s_p) {
+    const int C = P.C, lane = threadIdx.x & (kWave - 1);
     float WR = 0.f, WP = 0.f;
-    int LR = -1, LP = -1;
-    int cs = INT_MAX;
-    float base = 0.f;
-    bool use_r;
-    float W, target;
-    if (C <= NT) {
-        // One record per thread: both scans, both maxima and the crossing
-        // in two workgroup exchanges.
-        __shared__ float s_tot[2][NT / kWave];
-        __shared__ int s_max[2][NT / kWave];
-        __shared__ int s_first[NT / kWave];
-        __shared__ float s_base[NT / kWave];
-        const int lane = tid & (kWave - 1), wv = tid / kWave;
-        float ir = wave_incl_scan(mine0.r, lane), ip = wave_incl_scan(mine0.p, lane);
-        const int mr = wave_max_int(mine0.last_r), mp = wave_max_int(mine0.last_p);
-        if (lane == kWave - 1) {
-            s_tot[0][wv] = ir;
-            s_tot[1][wv] = ip;
+    int LR = -1, LP = -1, late = 0;
+    for (int q0 = 0; q0 < C; q0 += kWave) {
+        const int qq = q0 + lane;
+        float r = 0.f, p = 0.f;
+        int lr = -1, lp = -1;
+        if (qq == q) {
+            r = own.r;
+            p = own.p;
+            lr = own.lr;
+            lp = own.lp;
+        } else if (qq < C) {
+            const PartRec* rec = P.parts + (size_t)b * C + qq;
+            uint64_t w0 = load_word(&rec->r), w1 = load_word(&rec->p);
+            for (int it = 0; ((w0 >> 32) == 0 || (w1 >> 32) == 0) && it < kSpinLimit; ++it) {
+                __builtin_amdgcn_s_sleep(2);
+                if ((w0 >> 32) == 0) w0 = load_word(&rec->r);
+                if ((w1 >> 32) == 0) w1 = load_word(&rec->p);
+            }
+            late |= (w0 >> 32) == 0 || (w1 >> 32) == 0;
+            r = __uint_as_float((uint32_t)w0);
+            p = __uint_as_float((uint32_t)w1);
+            lr = (int)(w0 >> 32) - 2;
+            lp = (int)(w1 >> 32) - 2;
         }
-        if (lane == 0) {
-            s_max[0][wv] = mr;
-            s_max[1][wv] = mp;
+        if (qq < C) {
+            s_r[qq] = r;
+            s_p[qq] = p;
+        }
+        WR += wave_sum(r);
+        WP += wave_sum(p);
+        LR = max(LR, wave_max_int(lr));
+        LP = max(LP, wave_max_int(lp));
+    }
+    Crossing x;
+    x.late = wave_max_int(late);
+    x.use_r = d.n < P.K && WR > 1e-12f;
+    x.W = x.use_r ? WR : WP;
+    x.last = x.use_r ? LR : LP;
+    x.target = P.resample_u[b] * x.W;
+    x.cs = INT_MAX;
+    x.base = 0.f;
+    if (x.late || !(x.W > 0.f)) return x;
+    float carry = 0.f;
+    for (int q0 = 0; q0 < C && x.cs == INT_MAX; q0 += kWave) {
+        const int qq = q0 + lane;
+        const float w = qq < C ? (x.use_r ? s_r[qq] : s_p[qq]) : 0.f;  // written by this lane
+        const float incl = carry + wave_incl_scan(w, lane);
+        const uint64_t hit = __ballot(qq < C && incl > x.target);
+        if (hit) {
+            const int f = __builtin_ctzll(hit);
+            x.cs = q0 + f;
+            x.base = __shfl(incl - w, f);
+        }
+        carry = __shfl(incl, kWave - 1);
+    }
+    return x;
+}
+
+template <int DT, bool VEC, Mode M, bool UNIT_T, bool SP>
+__global__ __launch_bounds__(NT) void accept_finish_kernel(Params P) {
+    const int per = M == kGreedy ? 1 : P.C;
+    const int b = blockIdx.x / per, q = blockIdx.x - b * per;
+    const bool writer = q == per - 1;
+    const Decision d = decide<DT, M, UNIT_T, SP>(P, b, writer);
+    if constexpr (M != kGreedy) {
+        if (d.bad) return;
+        __shared__ float4 s4[NT / kWave];
+        __shared__ int2 s2[NT / kWave];
+        __shared__ float s_r[kMaxParts], s_p[kMaxParts];
+        __shared__ Crossing s_x;
+        float wr[kRun], wp[kRun];
+        part_weights<DT, VEC, M, UNIT_T, SP>(P, b, d, q, wr, wp);
+        const int e0 = q * kPart + (int)threadIdx.x * kRun;
+        float tr = 0.f, tp = 0.f;
+        int lr = -1, lp = -1;
+#pragma unroll
+        for (int k = 0; k < kRun; ++k) {
+            tr += wr[k];
+            tp += wp[k];
+            if (wr[k] > 0.f) lr = e0 + k;
+            if (wp[k] > 0.f) lp = e0 + k;
+        }
+        float xr, xp;
+        const PartSums own = block_part_scan(tr, tp, lr, lp, s4, xr, xp);
+        if (threadIdx.x == 0) {
+            PartRec* rec = P.parts + (size_t)b * P.C + q;
+            store_word(&rec->r, own.r, own.lr + 2);
+            store_word(&rec->p, own.p, own.lp + 2);
+        }
+        if (threadIdx.x < kWave) {
+            const Crossing x = find_crossing(P, b, q, d, own, s_r, s_p);
+            if (threadIdx.x == 0) s_x = x;
         }
         __syncthreads();
-        // Same arithmetic as block_incl_scan: wave scan + earlier waves' totals.
-        float orr = 0.f, orp = 0.f;
-        for (int k = 0; k < NT / kWave; ++k) {
-            if (k < wv) {
-                orr += s_tot[0][k];
-                orp += s_tot[1][k];
-            }
-            LR = max(LR, s_max[0][k]);
-            LP = max(LP, s_max[1][k]);
-        }
-        {
-            float offr = 0.f, offp = 0.f;
-            for (int k = 0; k < NT / kWave - 1; ++k) {
-                offr += s_tot[0][k];
-                offp += s_tot[1][k];
-            }
-            WR = s_tot[0][NT / kWave - 1] + offr;  // the scan's last element
-            WP = s_tot[1][NT / kWave - 1] + offp;
-        }
-        ir += orr;
-        ip += orp;
-        use_r = res && WR > 1e-12f;
-        W = use_r ? WR : WP;
-        target = v * W;
-        const float incl = use_r ? ir : ip, w = use_r ? mine0.r : mine0.p;
-        const uint64_t bal = __ballot(tid < C && incl > target);
-        if (bal && lane == __builtin_ctzll(bal)) {
-            s_first[wv] = tid;
-            s_base[wv] = incl - w;
-        }
-        if (!bal && lane == 0) s_first[wv] = INT_MAX;
-        __syncthreads();
-        for (int k = 0; k < NT / kWave; ++k)
-            if (s_first[k] != INT_MAX) {
-                cs = s_first[k];
-                base = s_base[k];
-                break;
-            }
-        if (!(W > 0.f)) {
-            if (tid == 0) P.out_token[b] = D3D_TOKEN_EMPTY_DISTRIBUTION;
+        const Crossing x = s_x;
+        // out_token holds D3D_TOKEN_TIMEOUT from the stats launch until a
+        // workgroup that saw every record writes the token.
+        if (x.late) return;
+        if (!(x.W > 0.f) || x.cs == INT_MAX) {
+            if (writer && threadIdx.x == 0)
+                P.out_token[b] = x.W > 0.f ? (int64_t)x.last : (int64_t)D3D_TOKEN_EMPTY_DISTRIBUTION;
             return;
         }
-    } else {
-    for (int c0 = 0; c0 < C; c0 += NT) {
-        float r = 0.f, p = 0.f;
-        if (c0 + tid < C) {
-            const ResStat t = c0 == 0 ? mine0 : P.rstats[(size_t)b * C + c0 + tid];
-            r = t.r;
-            p = t.p;
-            LR = max(LR, t.last_r);
-            LP = max(LP, t.last_p);
-        }
-        const float ir = block_incl_scan(r, s_wave);
-        const float ip = block_incl_scan(p, s_wave);
-        if (tid == NT - 1) {
-            s_f[0] = ir;
-            s_f[1] = ip;
-        }
-        __syncthreads();
-        WR += s_f[0];
-        WP += s_f[1];
-        __syncthreads();
-    }
-    LR = block_max_int(LR, ri);
-    LP = block_max_int(LP, ri);
-    use_r = res && WR > 1e-12f;
-    W = use_r ? WR : WP;
-    target = v * W;
-    if (!(W > 0.f)) {
-        if (tid == 0) P.out_token[b] = D3D_TOKEN_EMPTY_DISTRIBUTION;
-        return;
-    }
-    float carry = 0.f;
-    for (int c0 = 0; c0 < C && cs == INT_MAX; c0 += NT) {
-        float w = 0.f;
-        if (c0 + tid < C) {
-            const ResStat t = c0 == 0 ? mine0 : P.rstats[(size_t)b * C + c0 + tid];
-            w = use_r ? t.r : t.p;
-        }
-        const float incl = carry + block_incl_scan(w, s_wave);
-        const int mine = (c0 + tid < C && incl > target) ? c0 + tid : INT_MAX;
-        const int first = block_min_int(mine, ri);
-        if (first != INT_MAX && first == c0 + tid) s_f[2] = incl - w;
-        if (tid == NT - 1) s_f[3] = incl;
-        __syncthreads();
-        if (first != INT_MAX) {
-            cs = first;
-            base = s_f[2];
-        }
-        carry = s_f[3];
-        __syncthreads();
-    }
-    }
-    int token;
-    if (cs == INT_MAX) {
-        token = use_r ? LR : LP;
-    } else {
-        // Contiguous ownership: thread tid holds entries first..first+L-1.
-        // Sub-chunk cs: thread tid owns entries first..first+E-1.
-        const int first = cs * (NT * E) + tid * E;
-        float xt[E], xq[E];
-        load_tile<DT, VEC, false, E>(row_ptr<DT>(P.target, (size_t)b * (K + 1) + d.n, V), V, first, E,
-                                     fill_value<M>(), xt);
-        if (res && !SP)
-            load_tile<DT, VEC, false, E>(row_ptr<DT>(P.draft, (size_t)b * K + d.n, V), V, first, E,
-                                         fill_value<M>(), xq);
-        float w[E];
-        if constexpr (SP) {
-            __shared__ float buf[NT * E];
-            __shared__ int s_id[kMaxS];
-            __shared__ float s_q[kMaxS];
-#pragma unroll
-            for (int l = 0; l < E; ++l) buf[tid * E + l] = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
-            if (use_r) sparse_subtract(P, b, d.n, d.Sq, cs * (NT * E), NT * E, buf, s_id, s_q);
-            else __syncthreads();
-#pragma unroll
-            for (int l = 0; l < E; ++l) w[l] = use_r ? fmaxf(buf[tid * E + l], 0.f) : buf[tid * E + l];
-        }
-        float tsum = 0.f;
-#pragma unroll
-        for (int l = 0; l < E; ++l) {
-            if constexpr (!SP) {
-                const float p = prob_of<M, UNIT_T>(xt[l], d.Mt, It, P.T);
-                w[l] = use_r ? fmaxf(p - prob_of<M, UNIT_T>(xq[l], d.Mq, Iq, P.T), 0.f) : p;
-            }
-            tsum += w[l];
-        }
-        const float incl = block_incl_scan(tsum, s_wave);
-        float run = base + (incl - tsum);
+        if (x.cs != q) return;
+        // This part holds the crossing: scan its entries in index order.
+        float run = x.base + (x.use_r ? xr : xp);
         int found = INT_MAX, lastpos = -1;
 #pragma unroll
-        for (int l = 0; l < E; ++l) {
-            run += w[l];
-            if (w[l] > 0.f) {
-                lastpos = first + l;
-                if (found == INT_MAX && run > target) found = first + l;
+        for (int k = 0; k < kRun; ++k) {
+            const float w = x.use_r ? wr[k] : wp[k];
+            run += w;
+            if (w > 0.f) {
+                lastpos = e0 + k;
+                if (found == INT_MAX && run > x.target) found = e0 + k;
             }
         }
-        found = block_min_int(found, ri);
-        lastpos = block_max_int(lastpos, ri);
-        token = found != INT_MAX ? found : lastpos;
+        block_min_max(found, lastpos, s2);
+        if (threadIdx.x == 0) P.out_token[b] = found != INT_MAX ? found : lastpos;
     }
-    if (tid == 0) P.out_token[b] = token;
-}
-
-template <int DT, bool VEC, Mode M, bool SP>
-__global__ __launch_bounds__(NT) void accept_resample_kernel(Params P) {
-    __shared__ float s_wave[NT / kWave];
-    __shared__ float s_f[4];
-    __shared__ int s_i[2];
-    __shared__ int ri[NT / kWave];
-    if (P.T == 1.0f)
-        resample_body<DT, VEC, M, true, SP>(P, blockIdx.x, s_wave, s_f, s_i, ri);
-    else
-        resample_body<DT, VEC, M, false, SP>(P, blockIdx.x, s_wave, s_f, s_i, ri);
 }
 
 struct Layout {
-    size_t stats, dec, rstats, xtok, total;
+    size_t stats, xtok, zsp, parts, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 static int num_chunks(int64_t V) { return (int)((V + kChunk - 1) / kChunk); }
-// Vectors per thread in phase-2/3 chunks: aim for >= ~128 workgroups per
-// launch with as few redundant row merges as possible.
-static int pick_nv2(int B) { return B >= 4 ? 4 : (B >= 2 ? 2 : 1); }
-static int num_subchunks(int64_t V, int dtype) {
-    const int ch = NT * (dtype == D3D_DTYPE_F32 ? 4 : 8);
-    return (int)((V + ch - 1) / ch);
-}
 
 static Layout layout(int B, int K, int64_t V) {
     Layout l;
     const size_t C = (size_t)num_chunks(V), R = 2 * (size_t)K + 1;
-    const size_t C2 = (size_t)num_subchunks(V, D3D_DTYPE_F32);  // the larger count of the two dtypes
     l.stats = 0;
-    l.dec = align256((size_t)B * R * C * sizeof(RowStat));
-    l.rstats = l.dec + align256((size_t)B * sizeof(Decision));
-    l.xtok = l.rstats + align256((size_t)B * C2 * sizeof(ResStat));
-    l.total = l.xtok + align256((size_t)B * R * sizeof(float));
+    l.xtok = align256((size_t)B * R * C * sizeof(RowStat));
+    l.zsp = l.xtok + align256((size_t)B * R * sizeof(float));
+    l.parts = l.zsp + align256((size_t)B * K * sizeof(float));
+    l.total = l.parts + align256((size_t)B * C * sizeof(PartRec));
     return l;
 }
 
+template <int DT, bool VEC, bool SP, Mode M, bool UNIT_T>
+static void launch_mode(const Params& P, hipStream_t stream) {
+    const dim3 grid_stats(P.C, P.Rm, P.B);
+    hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, M>), grid_stats, dim3(NT), 0, stream, P);
+    const int per = M == kGreedy ? 1 : P.C;
+    hipLaunchKernelGGL((accept_finish_kernel<DT, VEC, M, UNIT_T, SP>), dim3(P.B * per), dim3(NT), 0, stream, P);
+}
+
 template <int DT, bool VEC, bool SP>
-static hipError_t launch(const Params& P, Mode mode, int B, hipStream_t stream) {
-    const dim3 block(NT);
-    const dim3 grid_dec(mode == kGreedy ? 1 : (P.C2 + P.nv2 - 1) / P.nv2, B);
-    // Target rows 0..K, then (dense proposals) draft rows.
-    const dim3 grid_stats(P.C, (mode == kGreedy || SP) ? P.K + 1 : 2 * P.K + 1, B);
+static hipError_t launch(const Params& P, Mode mode, hipStream_t stream) {
     switch (mode) {
         case kGreedy:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kGreedy>), grid_stats, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kGreedy, false>), grid_dec, block, 0, stream, P);
-            return hipGetLastError();
+            launch_mode<DT, VEC, SP, kGreedy, true>(P, stream);
+            break;
         case kLogits:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kLogits>), grid_stats, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kLogits, SP>), grid_dec, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kLogits, SP>), dim3(B), block, 0, stream, P);
-            return hipGetLastError();
+            if (P.T == 1.0f)
+                launch_mode<DT, VEC, SP, kLogits, true>(P, stream);
+            else
+                launch_mode<DT, VEC, SP, kLogits, false>(P, stream);
+            break;
         default:
-            hipLaunchKernelGGL((accept_stats_kernel<DT, VEC, kProbs>), grid_stats, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_decide_kernel<DT, VEC, kProbs, SP>), grid_dec, block, 0, stream, P);
-            hipLaunchKernelGGL((accept_resample_kernel<DT, VEC, kProbs, SP>), dim3(B), block, 0, stream, P);
-            return hipGetLastError();
+            launch_mode<DT, VEC, SP, kProbs, true>(P, stream);
+            break;
     }
+    return hipGetLastError();
 }
 
 // Shared by the dense and sparse entry points: validation, workspace carving
@@ -668,15 +629,15 @@ static int run(const void* target, const void* draft, const int64_t* q_ids, cons
     P.uniforms = uniforms;
     P.resample_u = resample_u;
     P.T = input_kind == D3D_INPUT_LOGITS ? temperature : 1.0f;
+    P.B = B;
     P.K = K;
     P.V = (int)V;
     P.C = num_chunks(V);
-    P.nv2 = pick_nv2(B);
-    P.C2 = num_subchunks(V, dtype);
+    P.Rm = (greedy || sparse) ? K + 1 : 2 * K + 1;
     P.stats = reinterpret_cast<RowStat*>(ws + lay.stats);
-    P.dec = reinterpret_cast<Decision*>(ws + lay.dec);
-    P.rstats = reinterpret_cast<ResStat*>(ws + lay.rstats);
     P.xtok = reinterpret_cast<float*>(ws + lay.xtok);
+    P.zsp = reinterpret_cast<float*>(ws + lay.zsp);
+    P.parts = reinterpret_cast<PartRec*>(ws + lay.parts);
     P.q_ids = sparse ? q_ids : nullptr;
     P.q_probs = sparse ? q_probs : nullptr;
     P.S = sparse ? S : 0;
@@ -694,14 +655,14 @@ static int run(const void* target, const void* draft, const int64_t* q_ids, cons
     hipError_t err;
     if (dtype == D3D_DTYPE_F32) {
         if (sparse)
-            err = vec ? launch<kF32, true, true>(P, mode, B, s) : launch<kF32, false, true>(P, mode, B, s);
+            err = vec ? launch<kF32, true, true>(P, mode, s) : launch<kF32, false, true>(P, mode, s);
         else
-            err = vec ? launch<kF32, true, false>(P, mode, B, s) : launch<kF32, false, false>(P, mode, B, s);
+            err = vec ? launch<kF32, true, false>(P, mode, s) : launch<kF32, false, false>(P, mode, s);
     } else {
         if (sparse)
-            err = vec ? launch<kBF16, true, true>(P, mode, B, s) : launch<kBF16, false, true>(P, mode, B, s);
+            err = vec ? launch<kBF16, true, true>(P, mode, s) : launch<kBF16, false, true>(P, mode, s);
         else
-            err = vec ? launch<kBF16, true, false>(P, mode, B, s) : launch<kBF16, false, false>(P, mode, B, s);
+            err = vec ? launch<kBF16, true, false>(P, mode, s) : launch<kBF16, false, false>(P, mode, s);
     }
     return err == hipSuccess ? D3D_OK : (int)err;
 }

@@ -188,6 +188,8 @@ def _to_result(out: AcceptOutput) -> SpeculativeSampleResult:
         raise ValueError("draft token id outside the vocabulary")
     if token == _lib.D3D_TOKEN_EMPTY_DISTRIBUTION:
         raise RuntimeError("invalid multinomial distribution (sum of probabilities <= 0)")
+    if token == _lib.D3D_TOKEN_TIMEOUT:
+        raise RuntimeError("acceptance residual hand-off timed out")
     return SpeculativeSampleResult(
         accepted_draft_tokens=int(n),
         correction_token=out.out_token[:1].clone(),

@@ -52,6 +52,10 @@ extern "C" {
 /* Sentinels written to out_token[b] by the acceptance kernels. */
 #define D3D_TOKEN_EMPTY_DISTRIBUTION (-1) /* the resampling weights sum to zero */
 #define D3D_TOKEN_BAD_DRAFT (-2)          /* a draft token id lies outside [0, V) */
+/* The residual reduction's cross-workgroup wait (for the other parts of the
+ * same request) did not end within its bound of over 100 ms.  Not expected:
+ * workgroups are dispatched in order.  Every output but out_token is valid. */
+#define D3D_TOKEN_TIMEOUT (-3)
 
 /* Short description of a status code (static storage). */
 const char* d3d_status_string(int status);
@@ -139,7 +143,7 @@ int d3d_accept_fused_sparse(const void* target, int dtype, int input_kind,
  *
  * Sizes whose workspace (d3d_accept_workspace_bytes(B, K, V)) exceeds the
  * scratch return D3D_E_WORKSPACE before anything is launched: at K = 15 and
- * V = 151,936 that is B > 196.  The scratch needs no clearing between calls.
+ * V = 151,936 that is B > 213.  The scratch needs no clearing between calls.
  * The first call on a device looks the array's address up (once per
  * device, with that device current); make it before any graph capture.
  * Every call on one GPU shares that GPU's array: calls that overlap in time

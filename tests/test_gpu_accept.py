@@ -152,14 +152,22 @@ def test_u_equal_a_boundary_accepts_on_device():
             assert got["out_token"][0] == 1
 
 
-def test_workspace_reuse_across_calls_and_shapes():
-    """Counters are left at zero: repeated calls of different sizes agree with the oracle."""
-    for B, V in ((8, 151936), (1, 4096), (3, 70000), (8, 151936)):
-        inp = workloads.accept_inputs(B * 7 + V % 13, B=B, K=15, V=V, temperature=0.0)
-        got, t, _ = _run(inp, 0.0)
-        ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
-        np.testing.assert_array_equal(got["posterior"], ref["posterior"])
-        np.testing.assert_array_equal(got["out_token"], ref["out_token"])
+@pytest.mark.parametrize("T", [0.0, 1.0])
+def test_workspace_reuse_across_calls_and_shapes(T):
+    """One cached workspace serves calls of different sizes in turn (the
+    stats launch resets the hand-off counters and flags each call):
+    every call agrees with the oracle."""
+    for B, V in ((8, 151936), (1, 4096), (3, 70000), (8, 151936), (2, 1000)):
+        inp = workloads.accept_inputs(B * 7 + V % 13, B=B, K=15, V=V, temperature=T)
+        got, t, d = _run(inp, T)
+        if T == 0.0:
+            ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
+            np.testing.assert_array_equal(got["posterior"], ref["posterior"])
+            np.testing.assert_array_equal(got["out_token"], ref["out_token"])
+        else:
+            ref = oracle.accept_dense(t.numpy(), d.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                                      inp.resample_u.numpy(), kind=oracle.KIND_LOGITS, temperature=T)
+            _check_stochastic(got, ref, min_certified=0.5)
 
 
 def test_verify_speculative_block_reference_surface():
