@@ -55,13 +55,16 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # (two passes of `bench.py --no-cpu-baseline --no-models --calibrate-copy`),
 # each counter scaled by what it reads for a plain 64 MiB device copy in the
-# same process: FETCH_SIZE x 1.99921, WRITE_SIZE x 1.0.  They are measured
+# same process: FETCH_SIZE x 1.99930, WRITE_SIZE x 1.0.  They are measured
 # figures, not computed here; a kernel change needs a new counter pass.
 TRAFFIC = {
-    "c0_accept_t1": 20_703_291,
-    "c2_accept_b8": 162_642_841,
-    "c1_verify_attn": None,
-    "c2_verify_attn": None,
+    "c0_accept_t1": 20_563_524,
+    "c0_accept_greedy": 9_840_880,
+    "c1_verify_attn": 13_754_923,
+    "c2_verify_attn": 142_559_921,
+    "c2_accept_b8": 162_272_359,
+    "c3_draft_attn": 27_355_481,
+    "c3_confidence": 19_706_750,
 }
 
 
@@ -250,7 +253,7 @@ def kernel_rooflines(dev, calls: int):
     r, ms = run(acc(1, 1.0), 31 * 151936 * 4)
     out.append(_roof(0, "fused acceptance, batch 1, T=1", r.bytes, ms, 0.70, TRAFFIC["c0_accept_t1"]))
     r, ms = run(acc(1, 0.0), 31 * 151936 * 4)
-    out.append(_roof(0, "fused acceptance, batch 1, greedy", r.bytes, ms, 0.70))
+    out.append(_roof(0, "fused acceptance, batch 1, greedy", r.bytes, ms, 0.70, TRAFFIC["c0_accept_greedy"]))
     r, ms = run(lambda i: AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234 + i, num_pages=256), 8_716_804)
     out.append(_roof(1, "block-verify attention, batch 1, prefix 2048", r.bytes, ms, 0.60,
                      TRAFFIC["c1_verify_attn"], r.flops))
@@ -261,9 +264,10 @@ def kernel_rooflines(dev, calls: int):
     r, ms = run(acc(8, 1.0), 248 * 151936 * 4)
     out.append(_roof(2, "fused acceptance, batch 8, T=1", r.bytes, ms, 0.70, TRAFFIC["c2_accept_b8"]))
     r, ms = run(lambda i: AttnStep([1024 + 16] * 4, 16, 16, 8, 16, False, dev, seed=77 + i), 17_564_688)
-    out.append(_roof(3, "draft block attention, batch 4, prefix 1024", r.bytes, ms, 0.60, None, r.flops))
+    out.append(_roof(3, "draft block attention, batch 4, prefix 1024", r.bytes, ms, 0.60, TRAFFIC["c3_draft_attn"],
+                     r.flops))
     r, ms = run(lambda i: ConfStep(4, 16, 151936, 4, dev, seed=5 + i), 19_447_808)
-    out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", r.bytes, ms, 0.70))
+    out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", r.bytes, ms, 0.70, TRAFFIC["c3_confidence"]))
     del r
     torch.cuda.empty_cache()
     return out
