@@ -16,10 +16,10 @@ exactly one token and K tokens are K steps.  steps/s counts decode
 iterations over their wall time (admission and prefill excluded).
 
 ``rooflines`` lists the kernels each configuration names, each timed with
-HIP events on its launch stream over repeated calls; every call reads the
-next of several input sets totalling over 640 MB, so its inputs come from
-HBM rather than the 256 MB memory-side cache; ``frac`` = algorithmic bytes /
-call duration / 8 TB/s:
+HIP events over repeated calls replayed from one HIP graph (the form the
+engine runs them in); every call reads the next of several input sets
+totalling over 640 MB, so its inputs come from HBM rather than the 256 MB
+memory-side cache; ``frac`` = algorithmic bytes / call duration / 8 TB/s:
 
 * config 0: fused acceptance, batch 1, 16 target + 15 draft fp32 rows over
   V = 151,936 at T = 1 (18,840,064 B) and greedy (16 rows, 9,723,904 B);
@@ -83,7 +83,14 @@ def _parse():
     return ap.parse_args()
 
 
-class AcceptStep:
+class _Bound:
+    """A pre-bound C-ABI call whose last argument is the HIP stream."""
+
+    def bind_stream(self, handle: int) -> None:
+        self.args = self.args[:-1] + (handle,)
+
+
+class AcceptStep(_Bound):
     """Pre-bound fused-acceptance call (no Python-side allocation per call)."""
 
     def __init__(self, inp, temperature: float, dev):
@@ -122,7 +129,7 @@ class AcceptStep:
             self._check(st, "d3d_accept_fused")
 
 
-class AttnStep:
+class AttnStep(_Bound):
     """Pre-bound paged attention call (verify: causal block; draft: bidirectional)."""
 
     def __init__(self, lens, Q, Hq, Hkv, page_size, causal: bool, dev, seed=0, num_pages=None):
@@ -160,7 +167,7 @@ class AttnStep:
             self._check(st, "paged attention")
 
 
-class ConfStep:
+class ConfStep(_Bound):
     """Pre-bound confidence / top-k unmask call over [B, Q, V] bf16 logits
     (the greedy denoise iteration of the draft block)."""
 
@@ -185,6 +192,36 @@ class ConfStep:
         st = self.lib.d3d_confidence_topk_unmask(*self.args)
         if st:
             self._check(st, "d3d_confidence_topk_unmask")
+
+
+def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40) -> float:
+    """Average milliseconds per call with the calls replayed from a HIP graph
+    (the form the engine runs them in) of ``per_graph`` consecutive calls
+    cycling through the input sets: events on the replay stream, bracketed
+    by synchronisations."""
+    s = torch.cuda.Stream(dev)
+    for c in r.calls:
+        c.bind_stream(s.cuda_stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for c in r.calls:
+            c()
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(per_graph):
+                r()
+        for _ in range(max(1, -(-warmup // per_graph))):
+            g.replay()
+        torch.cuda.synchronize(dev)
+        reps = max(1, -(-calls // per_graph))
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(s)
+        for _ in range(reps):
+            g.replay()
+        end.record(s)
+        torch.cuda.synchronize(dev)
+    del g
+    return start.elapsed_time(end) / (reps * per_graph)
 
 
 def time_calls(fn, steps: int, warmup: int, dev) -> float:
@@ -247,7 +284,7 @@ def kernel_rooflines(dev, calls: int):
 
     def run(make, set_bytes):
         r = Rotating(make, set_bytes)
-        ms = time_calls(r, calls, warm, dev)
+        ms = time_graph(r, calls, warm, dev)
         return r, ms
 
     r, ms = run(acc(1, 1.0), 31 * 151936 * 4)
@@ -306,7 +343,10 @@ def e2e_bench(dev, new_tokens: int, warm_tokens: int):
     eng = Engine(QWEN3_8B, D3D_1P7B, anchor_num=1, pages=64, seed=42)
     g = torch.Generator().manual_seed(9)
     prompts = torch.randint(0, 151936, (4, 512), generator=g).tolist()
-    eng.generate(prompts, 4, max_new_tokens=max(warm_tokens, 1), ignore_eos=True)  # warm-up, graph captures
+    # The warm-up captures the block graphs at the timed run's page-table
+    # width (tables sized for its length), so the timed run only replays.
+    eng.min_table_tokens = 512 + new_tokens
+    eng.generate(prompts, 4, max_new_tokens=max(warm_tokens, 1), ignore_eos=True)
     res = eng.generate(prompts, 4, max_new_tokens=new_tokens, ignore_eos=True)
     del eng
     torch.cuda.empty_cache()

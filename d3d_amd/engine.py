@@ -120,6 +120,10 @@ class Engine:
             raise ValueError("fast_miss_anchors must be nonnegative")
         if draft_microbatch < 1:
             raise ValueError("draft_microbatch must be positive")
+        # generate sizes every page table for at least this many tokens per
+        # request (prompt + output), so that the graphs one call captures
+        # (keyed by table width) serve a later, longer call too.
+        self.min_table_tokens = 0
         self.fast_miss_anchors = fast_miss_anchors
         self.backup, self.seed = backup, seed
         self.K, self.A, self.micro = block_size, anchor_num, draft_microbatch
@@ -294,7 +298,8 @@ class Engine:
         ps = self.target.page_size
         A_max = max(self.A, self.fast_miss_anchors)
         Qp = K * (1 + A_max * (K - 1) + 1)
-        width = -(-(max(len(p) for p in prompts) + max_new_tokens + Qp + K) // ps)
+        need = max(max(len(p) for p in prompts) + max_new_tokens, self.min_table_tokens)
+        width = -(-(need + Qp + K) // ps)
         self.target.width = self.draft.width = width
         waiting = iter(enumerate(prompts))
         running: List[Sequence] = []

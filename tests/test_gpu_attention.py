@@ -93,6 +93,9 @@ def test_draft_block_bidirectional_qwen3_1p7b():
         ([130, 64, 65], 1, 64, 8, 16, True),  # decode-shaped, 8 heads per group
         ([500], 16, 8, 8, 32, False),    # MHA group of 1
         ([9000], 16, 32, 8, 16, True),   # long context, many splits
+        ([3000], 16, 32, 8, 16, True),   # 24 two-tile splits: the 24-slot combine
+        ([4000], 16, 32, 8, 16, True),   # 32 two-tile splits: the 32-slot combine
+        ([1416] * 4, 16, 16, 8, 16, False),  # draft shape, 23 one-tile splits: 24 slots
     ],
 )
 def test_shapes_and_edges(lens, Q, Hq, Hkv, ps, causal):
