@@ -497,7 +497,7 @@ def main():
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); "
-              "multi-GPU runs are not part of this build", file=sys.stderr)
+              "the path runs on a single MI355X here", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)

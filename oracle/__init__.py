@@ -1,7 +1,7 @@
 """ORACLE -- test infrastructure only.
 
-CPU restatements of D3D's per-step hot path, used as the checker for the
-gfx950 kernels.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+CPU restatements of D3D's per-step hot path, against which the tests compare
+the gfx950 kernels.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this package; the product
 (``d3d_amd``) never does.
 

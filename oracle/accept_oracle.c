@@ -2,8 +2,8 @@
  * ORACLE -- test infrastructure only.
  *
  * A CPU restatement, in double precision, of D3D's per-step acceptance
- * arithmetic.  It is the checker for the HIP kernels in d3d_amd/csrc and is
- * never linked into, called by, or shipped with the product path: only
+ * arithmetic.  The tests compare the HIP kernels in d3d_amd/csrc against it;
+ * it is never linked into, called by, or shipped with the product path: only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
  *
  * Reference behaviour restated here (paths relative to the D3D repository):
