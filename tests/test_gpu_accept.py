@@ -152,6 +152,28 @@ def test_u_equal_a_boundary_accepts_on_device():
             assert got["out_token"][0] == 1
 
 
+@pytest.mark.parametrize("K,V", [(1, 8195), (127, 8195), (127, 1000), (15, 1), (3, 4096)])
+@pytest.mark.parametrize("T", [0.0, 1.0])
+def test_block_length_and_vocabulary_extremes(K, V, T):
+    """K = 1 and K = 127 (the maximum: 255 rows merged per request), a
+    one-entry vocabulary and a vocabulary of exactly one chunk, greedy and
+    T = 1, against the oracle."""
+    inp = workloads.accept_inputs(K * 31 + V % 17, B=3, K=K, V=V, temperature=T)
+    got, t, d = _run(inp, T)
+    if T == 0.0:
+        ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
+        np.testing.assert_array_equal(got["posterior"], ref["posterior"])
+        np.testing.assert_array_equal(got["accepted"], ref["accepted"])
+        np.testing.assert_array_equal(got["out_token"], ref["out_token"])
+        np.testing.assert_array_equal(got["accept_mask"], ref["accept_mask"].astype(bool))
+    else:
+        ref = oracle.accept_dense(t.numpy(), d.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                                  inp.resample_u.numpy(), kind=oracle.KIND_LOGITS, temperature=T)
+        _check_stochastic(got, ref, min_certified=0.3 if V == 1 else 0.6)
+    if V == 1:  # every token is 0 and every draft accepted; the bonus draw is token 0
+        assert (got["accepted"] == K).all() and (got["out_token"] == 0).all()
+
+
 @pytest.mark.parametrize("T", [0.0, 1.0])
 def test_workspace_reuse_across_calls_and_shapes(T):
     """One cached workspace serves calls of different sizes in turn (the
