@@ -354,7 +354,7 @@ def e2e_bench(dev, new_tokens: int, warm_tokens: int):
 
 
 # -- CPU baselines (the oracle's fp32 torch-CPU restatements) -----------------
-def _median_ms(fn, budget_s: float, max_runs: int = 20, warmup: int = 2) -> tuple:
+def _median_ms(fn, budget_s: float, max_runs: int = 20, warmup: int = 3) -> tuple:
     for _ in range(warmup):
         fn()
     times = []
@@ -368,7 +368,7 @@ def _median_ms(fn, budget_s: float, max_runs: int = 20, warmup: int = 2) -> tupl
 
 def cpu_baselines(budget_s: float = 3.0):
     """Per configuration, all affinity cores and 1 thread: median of up to 20
-    runs after 2 warm-ups within about ``budget_s`` each."""
+    runs after 3 warm-ups within about ``budget_s`` each."""
     from d3d_amd import workloads
     from d3d_amd.model import D3D_1P7B
     from oracle import model_ref, torch_ref
