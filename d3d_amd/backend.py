@@ -99,7 +99,7 @@ class Runner:
                                      else seed)
         self.kv = PagedKV(shape, num_pages, page_size, self.device)
         self.pool = self.kv.pool
-        self.stream = dedicated_stream(self.device)
+        self.stream = dedicated_stream(self.device, "draft" if draft else "target")
         self.use_graphs = use_graphs
         self._steps: Dict = {}
         self.width: Optional[int] = None  # fixed page-table width (graph replays), None = longest table

@@ -7,6 +7,14 @@ overlap, so they are created with hipExtStreamCreateWithCUMask: a stream
 with a CU mask gets a dedicated hardware queue.  The mask enables every CU
 (no partitioning) and the streams keep the default priority.
 
+Hardware queues are a scarce, per-device resource: past the number the
+scheduler keeps mapped, a process's queues are time-sliced.  So there is
+one dedicated stream per (device, role) for the life of the process, shared
+by every Runner of that role (an engine's target and its draft take
+different roles); engines built one after another reuse the same two
+queues instead of adding two each.  Runners of one role driven from several
+threads at once therefore serialise on their shared stream.
+
 Teardown: HIP objects this package creates -- the dedicated streams and the
 HIP graphs captured by model.BlockStep, with their workspaces -- are
 released by an interpreter-exit hook, in order (drain the devices, drop the
@@ -19,12 +27,13 @@ from __future__ import annotations
 import atexit
 import ctypes
 import weakref
-from typing import List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
 _hip: Optional[ctypes.CDLL] = None
 _streams: List[int] = []            # raw handles of the dedicated streams
+_pool: Dict[Tuple[int, str], torch.cuda.ExternalStream] = {}  # (device, role) -> stream
 _graph_owners: "weakref.WeakSet" = weakref.WeakSet()
 _hook_registered = False
 
@@ -62,6 +71,7 @@ def teardown() -> None:
         torch.cuda.synchronize()
     except Exception:
         pass
+    _pool.clear()
     if _streams:
         hip = _runtime()
         while _streams:
@@ -81,23 +91,32 @@ def _runtime() -> ctypes.CDLL:
     return _hip
 
 
-def dedicated_stream(device) -> torch.cuda.ExternalStream:
-    """A default-priority stream on its own hardware queue, covering all CUs.
+def dedicated_stream(device, role: str = "default") -> torch.cuda.ExternalStream:
+    """The default-priority stream with a hardware queue of its own for
+    (device, role), covering all CUs: created on the first request and
+    returned to every later one for the same pair.
 
     The stream lives until the process ends (graphs replayed on it may
     outlive any one owner); the exit hook destroys it.
     """
     device = torch.device(device)
-    n = torch.cuda.get_device_properties(device).multi_processor_count
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, role)
+    stream = _pool.get(key)
+    if stream is not None:
+        return stream
+    n = torch.cuda.get_device_properties(index).multi_processor_count
     words = (n + 31) // 32
     mask = (ctypes.c_uint32 * words)(*([0xFFFFFFFF] * words))
     if n % 32:
         mask[words - 1] = (1 << (n % 32)) - 1
     handle = ctypes.c_void_p()
-    with torch.cuda.device(device):
+    with torch.cuda.device(index):
         status = _runtime().hipExtStreamCreateWithCUMask(ctypes.byref(handle), words, mask)
     if status != 0:
         raise RuntimeError(f"hipExtStreamCreateWithCUMask failed with HIP error {status}")
     _ensure_hook()
     _streams.append(handle.value)
-    return torch.cuda.ExternalStream(handle.value, device=device)
+    stream = torch.cuda.ExternalStream(handle.value, device=torch.device("cuda", index))
+    _pool[key] = stream
+    return stream

@@ -138,6 +138,23 @@ def test_fast_backups_stay_lossless(backup):
     _same_up_to_near_tie(W, prompts, [o["tokens"] for o in want["outputs"]], [o["tokens"] for o in got["outputs"]])
 
 
+def test_engines_share_one_dedicated_stream_per_role():
+    """Engines built one after another reuse the process's two dedicated
+    streams (one hardware queue each) instead of adding two per engine, and
+    interleaved use of two engines on the shared streams gives each the
+    outputs it gives alone."""
+    a, b = _engine(41), _engine(43)
+    assert a.target.stream.cuda_stream == b.target.stream.cuda_stream
+    assert a.draft.stream.cuda_stream == b.draft.stream.cuda_stream
+    assert a.target.stream.cuda_stream != a.draft.stream.cuda_stream
+    prompts = torch.randint(0, 999, (2, 24), generator=torch.Generator().manual_seed(5)).tolist()
+    first = [o["tokens"] for o in a.generate(prompts, 2, max_new_tokens=12, ignore_eos=True)["outputs"]]
+    other = [o["tokens"] for o in b.generate(prompts, 2, max_new_tokens=12, ignore_eos=True)["outputs"]]
+    again = [o["tokens"] for o in a.generate(prompts, 2, max_new_tokens=12, ignore_eos=True)["outputs"]]
+    alone = [o["tokens"] for o in _engine(43).generate(prompts, 2, max_new_tokens=12, ignore_eos=True)["outputs"]]
+    assert again == first and other == alone
+
+
 def test_predict_and_verify_surfaces():
     """_predict returns {seq_id: {(n, anchor or None): (block, top)}} with A
     branches per accepted count and the all-accepted one; _verify equals
