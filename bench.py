@@ -194,6 +194,65 @@ class ConfStep(_Bound):
             self._check(st, "d3d_confidence_topk_unmask")
 
 
+class GemmStep(_Bound):
+    """Pre-bound 64-row projection Y = X W^T: d3d_gemm_rows64 with its split
+    count (fp32 partials when it splits K; summing them is the next fused
+    kernel's job and is not timed here), or hipBLASLt (torch.mm into a
+    preallocated bf16 output)."""
+
+    def __init__(self, M, N, K, dev, hip: bool, seed=0):
+        from d3d_amd import _lib
+        self.lib = _lib.load()
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        self.w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        self.hip = hip
+        self.splits = self.lib.d3d_gemm_rows64_splits(N, K)
+        self.y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        self.parts = torch.empty(self.splits, M, N, dtype=torch.float32, device=dev)
+        self.args = (self.x.data_ptr(), self.w.data_ptr(), self.y.data_ptr(), self.parts.data_ptr(), M, N, K,
+                     self.splits, torch.cuda.current_stream(dev).cuda_stream)
+        self._check = _lib.check
+        self.bytes = N * K * 2 + M * K * 2 + M * N * 2
+
+    def __call__(self):
+        if self.hip:
+            st = self.lib.d3d_gemm_rows64(*self.args)
+            if st:
+                self._check(st, "d3d_gemm_rows64")
+        else:
+            torch.mm(self.x, self.w.t(), out=self.y)
+
+
+# The 64-row projections of the two models (N, K): qkv, o, gate-up, down.
+GEMM_SHAPES = {
+    "target qkv": (6144, 4096), "target o": (4096, 4096), "target gate_up": (24576, 4096),
+    "target down": (4096, 12288), "draft qkv": (4096, 2048), "draft o": (2048, 2048),
+    "draft gate_up": (12288, 2048), "draft down": (2048, 6144),
+}
+
+
+def gemm_rows64_bench(dev, calls: int):
+    """64-row projections on d3d_gemm_rows64 beside hipBLASLt, weights
+    streamed from HBM (rotating copies), graph-replayed."""
+    warm = max(calls // 10, 3)
+    out = []
+    for name, (N, K) in GEMM_SHAPES.items():
+        row = {"shape": name, "M": 64, "N": N, "K": K}
+        for hip in (True, False):
+            r = Rotating(lambda i: GemmStep(64, N, K, dev, hip, seed=i), N * K * 2)
+            ms = time_graph(r, calls, warm, dev)
+            key = "hip" if hip else "hipblaslt"
+            row[key + "_us"] = round(ms * 1e3, 2)
+            row[key + "_GBps"] = round(r.bytes / (ms * 1e-3) / 1e9, 1)
+            if hip:
+                row["splits"] = r.calls[0].splits
+            del r
+            torch.cuda.empty_cache()
+        out.append(row)
+    return out
+
+
 def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40) -> float:
     """Average milliseconds per call with the calls replayed from a HIP graph
     (the form the engine runs them in) of ``per_graph`` consecutive calls
@@ -515,6 +574,8 @@ def main():
 
     roofs = kernel_rooflines(dev, args.kernel_calls)
     print(f"kernels timed ({len(roofs)})", file=sys.stderr, flush=True)
+    gemms = gemm_rows64_bench(dev, args.kernel_calls)
+    print("64-row projections timed", file=sys.stderr, flush=True)
     top = next(r for r in roofs if r["kernel"].startswith("fused acceptance, batch 8"))
     out = {
         "metric": "accept-kernel µs & HBM GB/s; verify-attn TFLOP/s; draft+verify steps/s at 1 GPU",
@@ -542,6 +603,7 @@ def main():
         "roofline": {k: top[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")} | {
             "kernel": top["kernel"], "algorithmic_bytes": top["algorithmic_bytes"], "us": top["us"]},
         "rooflines": roofs,
+        "gemm_rows64": gemms,
     }
     if not args.no_models:
         out["draft_block_step_ms"] = round(draft_block_bench(dev), 3)

@@ -20,6 +20,11 @@
 // Rows are bf16; the head dim is 128, split between lane l (entry l) and
 // lane l + 64 of a wave (entry l + 64), which are exactly the pairs the
 // rotate-half RoPE mixes.
+//
+// The *_parts forms take their GEMM input as the fp32 partials of a K-split
+// GEMM (d3d_gemm_rows64, [splits][T][width]): each entry is the partials
+// summed in split order and rounded to bf16, the value a bf16 GEMM output
+// holds, and then everything proceeds as in the bf16 form.
 #include "d3d_common.hpp"
 #include "../../include/d3d_hip.h"
 
@@ -34,11 +39,46 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 __device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Entries e .. e + 7 of a K-split product: the fp32 partials summed in
+// split order, rounded to bf16 and packed in pairs like a bf16 row.
+__device__ __forceinline__ u32x4 sum_parts8(const float* parts, int splits, size_t stride, size_t e) {
+    float a[8];
+    {
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(parts + e);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(parts + e + 4);
+        a[0] = p0.x; a[1] = p0.y; a[2] = p0.z; a[3] = p0.w;
+        a[4] = p1.x; a[5] = p1.y; a[6] = p1.z; a[7] = p1.w;
+    }
+    for (int sp = 1; sp < splits; ++sp) {
+        const float* q = parts + (size_t)sp * stride + e;
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(q);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(q + 4);
+        a[0] += p0.x; a[1] += p0.y; a[2] += p0.z; a[3] += p0.w;
+        a[4] += p1.x; a[5] += p1.y; a[6] += p1.z; a[7] += p1.w;
+    }
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+        o[h] = (uint32_t)f32_to_bf16_bits(a[2 * h]) | ((uint32_t)f32_to_bf16_bits(a[2 * h + 1]) << 16);
+    return o;
+}
+
+// One entry of a K-split product, as bf16 bits.
+__device__ __forceinline__ uint16_t sum_parts1(const float* parts, int splits, size_t stride, size_t e) {
+    float a = parts[e];
+    for (int sp = 1; sp < splits; ++sp) a += parts[(size_t)sp * stride + e];
+    return f32_to_bf16_bits(a);
+}
+
 // One workgroup per row of H entries (H a multiple of 8).  One wave per row
 // (no block reduction) measured slower -- 5.1 -> 7.2 us at 1088 x 2048 and
 // 3.8 -> 8.8 us at 64 x 4096 -- because it leaves a quarter of the waves to
 // hide the load latency.
-__global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, uint16_t* residual,
+template <bool PARTS>
+__global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restrict__ x, const float* __restrict__ parts,
+                                                         int splits, size_t stride, uint16_t* residual,
                                                          const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
                                                          int H, float eps) {
     const size_t row = blockIdx.x;
@@ -56,12 +96,13 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
         wreg[j] = *reinterpret_cast<const u32x4*>(w + vi * 8);
         const u32x4 r = *reinterpret_cast<const u32x4*>(residual + off);
         u32x4 a = {0u, 0u, 0u, 0u};
-        if (x) a = *reinterpret_cast<const u32x4*>(x + off);
+        if constexpr (PARTS) a = sum_parts8(parts, splits, stride, off);
+        else if (x) a = *reinterpret_cast<const u32x4*>(x + off);
         u32x4 rs;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             float lo = bf16_bits_to_f32(r[h] & 0xffffu), hi = bf16_bits_to_f32(r[h] >> 16);
-            if (x) {
+            if (PARTS || x) {
                 lo += bf16_bits_to_f32(a[h] & 0xffffu);
                 hi += bf16_bits_to_f32(a[h] >> 16);
             }
@@ -70,7 +111,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
             ss += lo * lo + hi * hi;
             rs[h] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
         }
-        if (x) *reinterpret_cast<u32x4*>(residual + off) = rs;
+        if (PARTS || x) *reinterpret_cast<u32x4*>(residual + off) = rs;
     }
     const float tot = block_sum<NT>(ss, red);
     const float rstd = rsqrtf(tot / (float)H + eps);
@@ -98,9 +139,10 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
 // (norm + rope -> q_out), key heads (norm + rope -> k_cache) and value heads
 // (copy -> v_cache).  Lane l holds entries l and l + 64 of a head, the pair
 // the rotate-half RoPE mixes, and computes that pair's cos / sin itself.
-template <bool DRAFT_ROPE>
+template <bool DRAFT_ROPE, bool PARTS>
 __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
-    const uint16_t* __restrict__ qkv, const int64_t* __restrict__ positions, const uint16_t* __restrict__ qn,
+    const uint16_t* __restrict__ qkv, const float* __restrict__ parts, int splits, size_t stride,
+    const int64_t* __restrict__ positions, const uint16_t* __restrict__ qn,
     const uint16_t* __restrict__ kn, const float* __restrict__ inv_freq, uint16_t* __restrict__ q_out,
     uint16_t* k_cache, uint16_t* v_cache, const int64_t* __restrict__ slots, int Hq, int Hkv, float eps,
     int64_t num_slots) {
@@ -109,9 +151,16 @@ __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
     const int h = blockIdx.y * (NT / kWave) + (threadIdx.x >> 6);
     const int heads = Hq + 2 * Hkv;
     if (h >= heads) return;  // whole wave; no barrier in this kernel
-    const uint16_t* src = qkv + (t * (size_t)heads + h) * HD;
     // Every load of this wave at once.
-    const uint16_t a = src[lane], b = src[lane + 64];
+    const size_t e = (t * (size_t)heads + h) * HD;
+    uint16_t a, b;
+    if constexpr (PARTS) {
+        a = sum_parts1(parts, splits, stride, e + lane);
+        b = sum_parts1(parts, splits, stride, e + lane + 64);
+    } else {
+        a = qkv[e + lane];
+        b = qkv[e + lane + 64];
+    }
     const int64_t slot = slots[t];
     const bool store = slot >= 0 && slot < num_slots;
     if (h >= Hq + Hkv) {  // value head: copy into the cache
@@ -185,15 +234,77 @@ using namespace d3d;
 // add_rmsnorm and silu_mul move rows as 16-byte vectors.
 static bool unaligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 != 0; }
 
-extern "C" int d3d_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int T, int H,
-                               float eps, void* stream) {
+static int add_rmsnorm(const void* x, const float* parts, int splits, void* residual, const void* weight, void* out,
+                       int T, int H, float eps, void* stream) {
     if (T < 0 || H < 8 || H % 8 || H > 8 * 4 * layers::NT) return D3D_E_SHAPE;
     if (T == 0) return D3D_OK;
     if (!residual || !weight || !out) return D3D_E_NULL;
-    if (unaligned16(x) || unaligned16(residual) || unaligned16(weight) || unaligned16(out)) return D3D_E_UNSUPPORTED;
-    hipLaunchKernelGGL(layers::add_rmsnorm_kernel, dim3(T), dim3(layers::NT), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint16_t*>(x), static_cast<uint16_t*>(residual),
-                       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), H, eps);
+    if (unaligned16(x) || unaligned16(parts) || unaligned16(residual) || unaligned16(weight) || unaligned16(out))
+        return D3D_E_UNSUPPORTED;
+    const size_t stride = (size_t)T * H;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (parts)
+        hipLaunchKernelGGL(layers::add_rmsnorm_kernel<true>, dim3(T), dim3(layers::NT), 0, s, nullptr, parts, splits,
+                           stride, static_cast<uint16_t*>(residual), static_cast<const uint16_t*>(weight),
+                           static_cast<uint16_t*>(out), H, eps);
+    else
+        hipLaunchKernelGGL(layers::add_rmsnorm_kernel<false>, dim3(T), dim3(layers::NT), 0, s,
+                           static_cast<const uint16_t*>(x), nullptr, 0, stride, static_cast<uint16_t*>(residual),
+                           static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out), H, eps);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
+}
+
+extern "C" int d3d_add_rmsnorm(const void* x, void* residual, const void* weight, void* out, int T, int H,
+                               float eps, void* stream) {
+    return add_rmsnorm(x, nullptr, 0, residual, weight, out, T, H, eps, stream);
+}
+
+extern "C" int d3d_add_rmsnorm_parts(const float* parts, int splits, void* residual, const void* weight, void* out,
+                                     int T, int H, float eps, void* stream) {
+    if (splits < 1) return D3D_E_SHAPE;
+    if (!parts) return D3D_E_NULL;
+    return add_rmsnorm(nullptr, parts, splits, residual, weight, out, T, H, eps, stream);
+}
+
+static int qk_rope_append(const void* qkv, const float* parts, int splits, const int64_t* positions,
+                          const void* q_norm_w, const void* k_norm_w, const float* inv_freq, void* q_out,
+                          void* k_cache, void* v_cache, const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
+                          float eps, int draft_rope, int64_t num_slots, void* stream) {
+    if (T < 0 || Hq < 1 || Hkv < 1 || num_slots < 1) return D3D_E_SHAPE;
+    if (D != layers::HD) return D3D_E_UNSUPPORTED;
+    if (T == 0) return D3D_OK;
+    if ((!qkv && !parts) || !positions || !q_norm_w || !k_norm_w || !inv_freq || !q_out || !k_cache || !v_cache ||
+        !slot_mapping)
+        return D3D_E_NULL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* a = static_cast<const uint16_t*>(qkv);
+    const size_t stride = (size_t)T * (Hq + 2 * Hkv) * layers::HD;
+    const dim3 grid(T, (Hq + 2 * Hkv + layers::NT / kWave - 1) / (layers::NT / kWave));
+    const auto* qn = static_cast<const uint16_t*>(q_norm_w);
+    const auto* kn = static_cast<const uint16_t*>(k_norm_w);
+    auto* qo = static_cast<uint16_t*>(q_out);
+    auto* kc = static_cast<uint16_t*>(k_cache);
+    auto* vc = static_cast<uint16_t*>(v_cache);
+    if (parts) {
+        if (draft_rope)
+            hipLaunchKernelGGL((layers::qk_rope_append_kernel<true, true>), grid, dim3(layers::NT), 0, s, nullptr,
+                               parts, splits, stride, positions, qn, kn, inv_freq, qo, kc, vc, slot_mapping, Hq, Hkv,
+                               eps, num_slots);
+        else
+            hipLaunchKernelGGL((layers::qk_rope_append_kernel<false, true>), grid, dim3(layers::NT), 0, s, nullptr,
+                               parts, splits, stride, positions, qn, kn, inv_freq, qo, kc, vc, slot_mapping, Hq, Hkv,
+                               eps, num_slots);
+    } else {
+        if (draft_rope)
+            hipLaunchKernelGGL((layers::qk_rope_append_kernel<true, false>), grid, dim3(layers::NT), 0, s, a,
+                               nullptr, 0, stride, positions, qn, kn, inv_freq, qo, kc, vc, slot_mapping, Hq, Hkv,
+                               eps, num_slots);
+        else
+            hipLaunchKernelGGL((layers::qk_rope_append_kernel<false, false>), grid, dim3(layers::NT), 0, s, a,
+                               nullptr, 0, stride, positions, qn, kn, inv_freq, qo, kc, vc, slot_mapping, Hq, Hkv,
+                               eps, num_slots);
+    }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }
@@ -202,27 +313,20 @@ extern "C" int d3d_qk_rope_append(const void* qkv, const int64_t* positions, con
                                   const void* k_norm_w, const float* inv_freq, void* q_out, void* k_cache,
                                   void* v_cache, const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
                                   float eps, int draft_rope, int64_t num_slots, void* stream) {
-    if (T < 0 || Hq < 1 || Hkv < 1 || num_slots < 1) return D3D_E_SHAPE;
-    if (D != layers::HD) return D3D_E_UNSUPPORTED;
-    if (T == 0) return D3D_OK;
-    if (!qkv || !positions || !q_norm_w || !k_norm_w || !inv_freq || !q_out || !k_cache || !v_cache ||
-        !slot_mapping)
-        return D3D_E_NULL;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const auto* a = static_cast<const uint16_t*>(qkv);
-    const dim3 grid(T, (Hq + 2 * Hkv + layers::NT / kWave - 1) / (layers::NT / kWave));
-    if (draft_rope)
-        hipLaunchKernelGGL(layers::qk_rope_append_kernel<true>, grid, dim3(layers::NT), 0, s, a, positions,
-                           static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
-                           inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
-                           static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
-    else
-        hipLaunchKernelGGL(layers::qk_rope_append_kernel<false>, grid, dim3(layers::NT), 0, s, a, positions,
-                           static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w),
-                           inv_freq, static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
-                           static_cast<uint16_t*>(v_cache), slot_mapping, Hq, Hkv, eps, num_slots);
-    const hipError_t err = hipGetLastError();
-    return err == hipSuccess ? D3D_OK : (int)err;
+    if (!qkv) return D3D_E_NULL;
+    return qk_rope_append(qkv, nullptr, 0, positions, q_norm_w, k_norm_w, inv_freq, q_out, k_cache, v_cache,
+                          slot_mapping, T, Hq, Hkv, D, eps, draft_rope, num_slots, stream);
+}
+
+extern "C" int d3d_qk_rope_append_parts(const float* parts, int splits, const int64_t* positions,
+                                        const void* q_norm_w, const void* k_norm_w, const float* inv_freq,
+                                        void* q_out, void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                                        int T, int Hq, int Hkv, int D, float eps, int draft_rope,
+                                        int64_t num_slots, void* stream) {
+    if (splits < 1) return D3D_E_SHAPE;
+    if (!parts) return D3D_E_NULL;
+    return qk_rope_append(nullptr, parts, splits, positions, q_norm_w, k_norm_w, inv_freq, q_out, k_cache, v_cache,
+                          slot_mapping, T, Hq, Hkv, D, eps, draft_rope, num_slots, stream);
 }
 
 extern "C" int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream) {

@@ -8,16 +8,75 @@
                          the draft) and the KV-cache store of
                          serving/vendor/ssd/layers/attention.py:21-22, one launch
 * ``silu_mul``        -- SiluAndMul (serving/vendor/ssd/layers/activation.py:6-14)
+* ``project``         -- the decoder layer's F.linear for blocks of at most
+                         64 rows (the qkv, o and down projections of a verify
+                         or draft block), by a weight-streaming HIP GEMM whose
+                         K-split partials ``add_rmsnorm`` and
+                         ``qk_rope_append`` sum on the way in
 
 Each is one gfx950 kernel; there is no CPU path.
 """
 from __future__ import annotations
 
-from typing import Optional
+from dataclasses import dataclass
+from typing import Optional, Union
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
+
+ROWS64 = 64  # largest block project() runs on the HIP GEMM
+
+
+@dataclass(frozen=True)
+class SplitProduct:
+    """x @ w.T as ``splits`` fp32 partial products over K ranges,
+    ``parts`` [splits, M, N]; its value is bf16(sum of the splits in order)."""
+    parts: torch.Tensor
+    splits: int
+
+    @property
+    def shape(self):
+        return self.parts.shape[1:]
+
+    def value(self) -> torch.Tensor:
+        """The bf16 product (the splits summed in order, then rounded)."""
+        acc = self.parts[0].clone()
+        for s in range(1, self.splits):
+            acc += self.parts[s]
+        return acc.to(torch.bfloat16)
+
+
+Product = Union[torch.Tensor, SplitProduct]
+
+
+def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
+    """F.linear(x, weight) for bf16 x [M, K] and weight [N, K].
+
+    Blocks of at most 64 rows with N % 64 == 0 and K % 128 == 0 run
+    d3d_gemm_rows64; when it splits K the result is a SplitProduct for
+    add_rmsnorm or qk_rope_append to consume.  Other shapes use F.linear
+    (hipBLASLt).
+    """
+    M, K = x.shape
+    N = weight.shape[0]
+    if (M > ROWS64 or N % 64 or K % 128 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
+            or not x.is_contiguous() or not weight.is_contiguous()):
+        return F.linear(x, weight)
+    dev = _lib.require_device(x, weight)
+    lib = _lib.load()
+    splits = lib.d3d_gemm_rows64_splits(N, K)
+    if splits == 1:
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        st = lib.d3d_gemm_rows64(x.data_ptr(), weight.data_ptr(), y.data_ptr(), None, M, N, K, 1, _lib.stream_ptr(dev))
+        _lib.check(st, "d3d_gemm_rows64")
+        return y
+    parts = torch.empty(splits, M, N, dtype=torch.float32, device=dev)
+    st = lib.d3d_gemm_rows64(x.data_ptr(), weight.data_ptr(), None, parts.data_ptr(), M, N, K, splits,
+                             _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_gemm_rows64")
+    return SplitProduct(parts, splits)
 
 
 def _bf16_rows(t: torch.Tensor, name: str) -> None:
@@ -25,13 +84,16 @@ def _bf16_rows(t: torch.Tensor, name: str) -> None:
         raise ValueError(f"{name} must be a contiguous bf16 tensor")
 
 
-def add_rmsnorm(x: Optional[torch.Tensor], residual: torch.Tensor, weight: torch.Tensor, eps: float,
+def add_rmsnorm(x: Optional[Product], residual: torch.Tensor, weight: torch.Tensor, eps: float,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = RMSNorm(x + residual) * weight; residual <- bf16(x + residual) in place.
 
     With ``x`` None the residual is normalised as it is and not written.
-    Rows are the last dimension of ``residual`` (H <= 8192, H % 8 == 0).
+    ``x`` may be a SplitProduct of ``project``.  Rows are the last dimension
+    of ``residual`` (H <= 8192, H % 8 == 0).
     """
+    if isinstance(x, SplitProduct):
+        return _add_rmsnorm_parts(x, residual, weight, eps, out)
     dev = _lib.require_device(x, residual, weight, out)
     _bf16_rows(residual, "residual")
     _bf16_rows(weight, "weight")
@@ -55,18 +117,26 @@ def add_rmsnorm(x: Optional[torch.Tensor], residual: torch.Tensor, weight: torch
     return out
 
 
-def qk_rope_append(qkv: torch.Tensor, positions: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor,
+def qk_rope_append(qkv: Product, positions: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor,
                    inv_freq: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                    slot_mapping: torch.Tensor, heads: int, kv_heads: int, eps: float, *, draft_rope: bool,
                    q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Normalise and rotate q and k, store k and v in the paged cache; returns q [T, Hq, D].
 
-    ``qkv`` [T, (Hq + 2 Hkv) * D] bf16, ``positions`` and ``slot_mapping``
-    [T] int64, caches [num_pages, page_size, Hkv, D] bf16.  Slots outside
-    the cache are skipped.
+    ``qkv`` [T, (Hq + 2 Hkv) * D] bf16, or a SplitProduct of ``project``;
+    ``positions`` and ``slot_mapping`` [T] int64, caches
+    [num_pages, page_size, Hkv, D] bf16.  Slots outside the cache are
+    skipped.
     """
-    dev = _lib.require_device(qkv, positions, q_norm, k_norm, inv_freq, k_cache, v_cache, slot_mapping)
-    _bf16_rows(qkv, "qkv")
+    split = qkv if isinstance(qkv, SplitProduct) else None
+    src = split.parts if split is not None else qkv
+    dev = _lib.require_device(src, positions, q_norm, k_norm, inv_freq, k_cache, v_cache, slot_mapping)
+    if split is not None:
+        if split.parts.dtype != torch.float32 or not split.parts.is_contiguous():
+            raise ValueError("split partials must be contiguous fp32")
+        qkv = split.parts[0]
+    else:
+        _bf16_rows(qkv, "qkv")
     P, ps, Hkv, D = k_cache.shape
     if v_cache.shape != k_cache.shape or Hkv != kv_heads:
         raise ValueError("cache shapes do not match the model's kv heads")
@@ -83,11 +153,16 @@ def qk_rope_append(qkv: torch.Tensor, positions: torch.Tensor, q_norm: torch.Ten
         raise ValueError("inv_freq must be fp32 [head_dim / 2]")
     if q_out is None:
         q_out = torch.empty(T, heads, D, dtype=torch.bfloat16, device=dev)
-    st = _lib.load().d3d_qk_rope_append(
-        qkv.data_ptr(), positions.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(), inv_freq.data_ptr(),
-        q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), T, heads, kv_heads, D,
-        float(eps), int(bool(draft_rope)), P * ps, _lib.stream_ptr(dev))
-    _lib.check(st, "d3d_qk_rope_append")
+    lib = _lib.load()
+    tail = (positions.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(), inv_freq.data_ptr(), q_out.data_ptr(),
+            k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(), T, heads, kv_heads, D, float(eps),
+            int(bool(draft_rope)), P * ps, _lib.stream_ptr(dev))
+    if split is not None:
+        st = lib.d3d_qk_rope_append_parts(split.parts.data_ptr(), split.splits, *tail)
+        _lib.check(st, "d3d_qk_rope_append_parts")
+    else:
+        st = lib.d3d_qk_rope_append(qkv.data_ptr(), *tail)
+        _lib.check(st, "d3d_qk_rope_append")
     return q_out
 
 
@@ -101,4 +176,27 @@ def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch
     T = gate_up.numel() // (2 * M)
     st = _lib.load().d3d_silu_mul(gate_up.data_ptr(), out.data_ptr(), T, M, _lib.stream_ptr(dev))
     _lib.check(st, "d3d_silu_mul")
+    return out
+
+
+def _add_rmsnorm_parts(x: SplitProduct, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                       out: Optional[torch.Tensor]) -> torch.Tensor:
+    dev = _lib.require_device(x.parts, residual, weight, out)
+    _bf16_rows(residual, "residual")
+    _bf16_rows(weight, "weight")
+    H = residual.shape[-1]
+    T = residual.numel() // H
+    if weight.numel() != H:
+        raise ValueError("weight must have one entry per hidden unit")
+    if x.parts.dtype != torch.float32 or not x.parts.is_contiguous() or tuple(x.parts.shape) != (x.splits, T, H):
+        raise ValueError("split partials must be contiguous fp32 [splits, T, H] matching the residual")
+    if out is None:
+        out = torch.empty_like(residual)
+    else:
+        _bf16_rows(out, "out")
+        if out.shape != residual.shape:
+            raise ValueError("out and residual shapes differ")
+    st = _lib.load().d3d_add_rmsnorm_parts(x.parts.data_ptr(), x.splits, residual.data_ptr(), weight.data_ptr(),
+                                           out.data_ptr(), T, H, float(eps), _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_add_rmsnorm_parts")
     return out

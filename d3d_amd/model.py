@@ -156,6 +156,9 @@ class Qwen3PagedModel(torch.nn.Module):
     def __init__(self, shape: ModelShape, device, *, draft: bool, seed: int = 0, init_std: float = 0.02):
         super().__init__()
         self.shape, self.draft, self.device = shape, draft, torch.device(device)
+        # Blocks of at most 64 tokens run the QKV, O and down projections on
+        # the weight-streaming HIP GEMM (layers.project) unless this is off.
+        self.rows64_gemm = True
         g = torch.Generator(device=self.device).manual_seed(seed)
         h, d, Hq, Hkv = shape.hidden, shape.head_dim, shape.heads, shape.kv_heads
 
@@ -190,6 +193,10 @@ class Qwen3PagedModel(torch.nn.Module):
         add + RMSNorm, QKV GEMM, fused q/k norm + RoPE + KV append, paged
         attention, O GEMM, fused add + RMSNorm, gate-up GEMM, fused SiLU-mul,
         down GEMM (the decoder layer of serving/vendor/ssd/models/qwen3.py).
+        Blocks of at most 64 tokens run the QKV, O and down GEMMs on the
+        weight-streaming HIP GEMM (layers.project, when ``rows64_gemm``), whose
+        K-split partials the next fused kernel sums; the gate-up GEMM and
+        larger blocks use F.linear.
         """
         B, Q = ids.shape
         s = self.shape
@@ -198,9 +205,10 @@ class Qwen3PagedModel(torch.nn.Module):
         residual = F.embedding(ids.reshape(-1), self.embed)  # updated in place below
         hs = torch.empty_like(residual)
         x = None
+        proj = ly.project if self.rows64_gemm else F.linear
         for li, L in enumerate(self.layers):
             ly.add_rmsnorm(x, residual, L["ln1"], s.eps, out=hs)
-            qkv = F.linear(hs, L["qkv"])
+            qkv = proj(hs, L["qkv"])
             q = ly.qk_rope_append(qkv, pos, L["qn"], L["kn"], self.inv_freq, kv.k[li], kv.v[li], slot_mapping,
                                   Hq, Hkv, s.eps, draft_rope=self.draft)
             if q_vis is None:
@@ -209,9 +217,9 @@ class Qwen3PagedModel(torch.nn.Module):
             else:
                 o = att.packed_block_attn(q.view(B, Q, Hq, d), kv.k[li], kv.v[li], context_lens, block_tables,
                                           q_vis, max_seqlen_k=max_context)
-            x = F.linear(o.reshape(B * Q, Hq * d), L["o"])
+            x = proj(o.reshape(B * Q, Hq * d), L["o"])
             ly.add_rmsnorm(x, residual, L["ln2"], s.eps, out=hs)
-            x = F.linear(ly.silu_mul(F.linear(hs, L["gate_up"])), L["down"])
+            x = proj(ly.silu_mul(F.linear(hs, L["gate_up"])), L["down"])
         out = ly.add_rmsnorm(x, residual, self.norm, s.eps)
         return out.reshape(B, Q, s.hidden)
 

@@ -434,6 +434,43 @@ int d3d_qk_rope_append(const void* qkv, const int64_t* positions, const void* q_
  */
 int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream);
 
+/*
+ * Projection of a block of at most 64 rows: Y[M, N] = X[M, K] W[N, K]^T with
+ * bf16 X (row-major, row stride K) and W (the [out, in] weight), fp32
+ * accumulation.  Replaces the F.linear of the decoder layer's qkv, o and
+ * down projections (serving/vendor/ssd/models/qwen3.py, as linear.py runs
+ * them) for verify and draft blocks.  1 <= M <= 64, N a multiple of 64, K a
+ * multiple of 128 * splits, X and W 16-byte aligned.  splits == 1 writes Y
+ * as bf16 [M, N]; splits > 1 (at most 16) writes the fp32 partial products
+ * of the splits' K ranges to parts [splits, M, N] instead, for
+ * d3d_add_rmsnorm_parts or d3d_qk_rope_append_parts to sum.  Y (or parts)
+ * must not overlap X or W.
+ */
+int d3d_gemm_rows64(const void* x, const void* w, void* y, float* parts, int M, int N, int K, int splits,
+                    void* stream);
+
+/* The split count d3d_gemm_rows64 is fastest with for an [N, K] weight (1 when N or K
+ * is not a multiple of 64 or 128). */
+int d3d_gemm_rows64_splits(int N, int K);
+
+/*
+ * d3d_add_rmsnorm with x given as the partials of d3d_gemm_rows64:
+ * x[t, i] = bf16(sum over s in order of parts[s, t, i]), parts
+ * [splits, T, H] fp32, 16-byte aligned.
+ */
+int d3d_add_rmsnorm_parts(const float* parts, int splits, void* residual, const void* weight, void* out, int T,
+                          int H, float eps, void* stream);
+
+/*
+ * d3d_qk_rope_append with qkv given as the partials of d3d_gemm_rows64:
+ * qkv[t, i] = bf16(sum over s in order of parts[s, t, i]), parts
+ * [splits, T, (Hq + 2 Hkv) * D] fp32.
+ */
+int d3d_qk_rope_append_parts(const float* parts, int splits, const int64_t* positions, const void* q_norm_w,
+                             const void* k_norm_w, const float* inv_freq, void* q_out, void* k_cache,
+                             void* v_cache, const int64_t* slot_mapping, int T, int Hq, int Hkv, int D,
+                             float eps, int draft_rope, int64_t num_slots, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

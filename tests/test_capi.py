@@ -73,3 +73,25 @@ def test_accept_rejects_small_workspace(d3d_lib):
     st = d3d_lib.d3d_accept_fused(p, p, 0, 0, p, p, p, 1.0, 1, 15, 151936,
                                   p, p, p, p, None, p, 64, None)
     assert st == -3
+
+
+def test_gemm_rows64_splits_and_argument_checks(d3d_lib):
+    lib = d3d_lib
+    # one round of 512 resident workgroups, at least two 128-wide k steps per split
+    assert lib.d3d_gemm_rows64_splits(4096, 12288) == 8
+    assert lib.d3d_gemm_rows64_splits(2048, 2048) == 8
+    assert lib.d3d_gemm_rows64_splits(2048, 6144) == 16
+    assert lib.d3d_gemm_rows64_splits(24576, 4096) == 1
+    assert lib.d3d_gemm_rows64_splits(12288, 2048) == 2
+    assert lib.d3d_gemm_rows64_splits(6144, 4096) == 4
+    assert lib.d3d_gemm_rows64_splits(2000, 2048) == 1 and lib.d3d_gemm_rows64_splits(2048, 100) == 1
+    null = ctypes.c_void_p(0)
+    dummy = ctypes.c_void_p(256)
+    for M, N, K, s in ((0, 64, 128, 1), (65, 64, 128, 1), (8, 100, 128, 1), (8, 64, 100, 1), (8, 64, 128, 2),
+                       (8, 64, 4096, 3), (8, 64, 4096, 32)):
+        assert lib.d3d_gemm_rows64(dummy, dummy, dummy, dummy, M, N, K, s, null) == -1, (M, N, K, s)
+    assert lib.d3d_gemm_rows64(null, dummy, dummy, dummy, 8, 64, 128, 1, null) == -4  # D3D_E_NULL
+    assert lib.d3d_gemm_rows64(dummy, dummy, null, dummy, 8, 64, 128, 1, null) == -4
+    assert lib.d3d_gemm_rows64(dummy, dummy, dummy, null, 8, 64, 256, 2, null) == -4
+    assert lib.d3d_add_rmsnorm_parts(dummy, 0, dummy, dummy, dummy, 4, 64, 1e-6, null) == -1
+    assert lib.d3d_add_rmsnorm_parts(null, 2, dummy, dummy, dummy, 4, 64, 1e-6, null) == -4
