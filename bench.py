@@ -234,11 +234,14 @@ GEMM_SHAPES = {
 
 def gemm_rows64_bench(dev, calls: int):
     """64-row projections on d3d_gemm_rows64 beside hipBLASLt, weights
-    streamed from HBM (rotating copies), graph-replayed."""
+    streamed from HBM (rotating copies), graph-replayed; ``project`` names
+    the one layers.project runs for the shape."""
+    from d3d_amd import layers as ly
     warm = max(calls // 10, 3)
     out = []
     for name, (N, K) in GEMM_SHAPES.items():
-        row = {"shape": name, "M": 64, "N": N, "K": K}
+        row = {"shape": name, "M": 64, "N": N, "K": K,
+               "project": "rows64" if ly.rows64_splits(N, K) else "hipblaslt"}
         for hip in (True, False):
             r = Rotating(lambda i: GemmStep(64, N, K, dev, hip, seed=i), N * K * 2)
             ms = time_graph(r, calls, warm, dev)

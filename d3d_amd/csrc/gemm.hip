@@ -143,14 +143,16 @@ using namespace d3d;
 extern "C" int d3d_gemm_rows64_splits(int N, int K) {
     if (N < gemm::TN || N % gemm::TN || K < gemm::TK || K % gemm::TK) return 1;
     // The most splits whose grid is one round of resident workgroups (two
-    // per CU with 64 KB of LDS each: 512) and leaves every split at least
-    // two k steps.  Measured on the qkv / o / gate-up / down shapes of both
-    // models at 64 rows (1, 2, 4, 8 and 16 splits each), it picks the
-    // fastest count on each of them (within 0.01 us on the draft qkv).
+    // per CU with 64 KB of LDS each: 512), leaving every split at least two
+    // k steps, and -- below K = 8192, where more splits buy less -- at most
+    // 16,384 partial floats per output row: the consumer of the product
+    // reads every partial back, about 1 us per 4 MB at 64 rows.  Measured
+    // on the 64-row projections of both models with 1-16 splits, counting
+    // that read, this is within 0.3 us of the fastest count on each.
     const int tiles = N / gemm::TN;
     int s = 1;
     while (s < gemm::kMaxSplits && tiles * 2 * s <= 512 && K % (gemm::TK * 2 * s) == 0 &&
-           K / (2 * s) >= 2 * gemm::TK)
+           K / (2 * s) >= 2 * gemm::TK && (K >= 8192 || (int64_t)2 * s * N <= 16384))
         s *= 2;
     return s;
 }

@@ -51,13 +51,29 @@ class SplitProduct:
 Product = Union[torch.Tensor, SplitProduct]
 
 
+def rows64_splits(N: int, K: int) -> int:
+    """The split count project() runs d3d_gemm_rows64 with for a 64-row
+    block times weight [N, K], or 0 where it uses hipBLASLt instead.
+
+    Only grids of exactly one or two workgroups per CU (256 CUs, N / 64
+    column tiles times the splits) beat hipBLASLt: fewer leave CUs idle (the
+    6144 x 4096 target qkv at 192), a round and a half leaves half of them
+    idle at the end (the 24576 x 4096 target gate-up at 384).
+    """
+    if N % 64 or K % 128:
+        return 0
+    splits = _lib.load().d3d_gemm_rows64_splits(N, K)
+    return splits if (N // 64) * splits in (256, 512) else 0
+
+
 def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
     """F.linear(x, weight) for bf16 x [M, K] and weight [N, K].
 
     Blocks of at most 64 rows with N % 64 == 0 and K % 128 == 0 run
-    d3d_gemm_rows64; when it splits K the result is a SplitProduct for
-    add_rmsnorm or qk_rope_append to consume.  Other shapes use F.linear
-    (hipBLASLt).
+    d3d_gemm_rows64 when its grid (N / 64 column tiles times the split
+    count) is one or two workgroups per CU; when it splits K the result is a
+    SplitProduct for add_rmsnorm or qk_rope_append to consume.  Other
+    shapes use F.linear (hipBLASLt).
     """
     M, K = x.shape
     N = weight.shape[0]
@@ -66,7 +82,9 @@ def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
         return F.linear(x, weight)
     dev = _lib.require_device(x, weight)
     lib = _lib.load()
-    splits = lib.d3d_gemm_rows64_splits(N, K)
+    splits = rows64_splits(N, K)
+    if not splits:
+        return F.linear(x, weight)
     if splits == 1:
         y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
         st = lib.d3d_gemm_rows64(x.data_ptr(), weight.data_ptr(), y.data_ptr(), None, M, N, K, 1, _lib.stream_ptr(dev))

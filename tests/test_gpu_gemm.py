@@ -104,8 +104,8 @@ def test_split_sum_kernels_equal_bf16_path():
     out_b = ly.add_rmsnorm(prod.value(), rb, nw, 1e-6)
     assert torch.equal(ra, rb) and torch.equal(out_a, out_b)
 
-    Hq, Hkv, D = 32, 8, 128
-    K = 4096
+    Hq, Hkv, D = 16, 8, 128  # the draft's qkv: 4096 x 2048, split 4 ways
+    K = 2048
     xq, wq = _operands(T, (Hq + 2 * Hkv) * D, K, seed=13)
     qkv = ly.project(xq, wq)
     assert isinstance(qkv, ly.SplitProduct)
@@ -134,3 +134,8 @@ def test_project_falls_back_beyond_64_rows_and_odd_shapes():
     assert isinstance(y, torch.Tensor) and torch.equal(y, F.linear(x, w))
     x2, w2 = _operands(16, 2000, 2048, seed=6)  # N not a multiple of 64
     assert torch.equal(ly.project(x2, w2), F.linear(x2, w2))
+    # grids other than one or two workgroups per CU go to hipBLASLt
+    x3, w3 = _operands(64, 6144, 4096, seed=7)  # 96 tiles x 2 splits
+    assert torch.equal(ly.project(x3, w3), F.linear(x3, w3))
+    x4, w4 = _operands(64, 2048, 6144, seed=8)  # 32 tiles x 8 splits
+    assert isinstance(ly.project(x4, w4), ly.SplitProduct)
