@@ -135,13 +135,6 @@ class Engine:
                             page_size=page_size, seed=seed + 1, use_graphs=use_graphs)
         if self.target.shape.vocab != self.draft.shape.vocab:
             raise ValueError("target and draft vocabularies must match")
-        # The target's verify forward runs beside the draft's packed predict
-        # (1088-row, compute-bound GEMMs).  There the 64-row weight-streaming
-        # GEMM (64 KB of LDS per workgroup) shares CUs badly: verify took
-        # 9.8-10.2 ms instead of 9.3 ms and neared the predict's 10.4 ms,
-        # while the draft's recovery gained 0.3 ms with it.  The target keeps
-        # hipBLASLt; the draft uses the HIP GEMM.
-        self.target.model.rows64_gemm = False
         if not 0 <= mask_id < self.draft.shape.vocab:
             raise ValueError(f"mask id {mask_id} outside the draft vocabulary")
 
