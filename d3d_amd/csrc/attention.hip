@@ -155,6 +155,11 @@ __device__ __forceinline__ float xor32_sum(float v) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Bits 0 .. n - 1 set: none for n <= 0, all 64 for n >= 64.
+__device__ __forceinline__ uint64_t bits_below(int n) {
+    return n <= 0 ? 0ull : n >= 64 ? ~0ull : (1ull << n) - 1ull;
+}
+
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -303,6 +308,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_split_kernel(Params P) {
     __shared__ __attribute__((aligned(16))) char lds[TILE * (ROWB + ROWB_V)];
     __shared__ int pages[kMaxSplitPages];
     __shared__ int s_lim[2][NW];
+    __shared__ uint32_t s_tiles[2][NW];
 
     // This lane's query row in row tile rt (wave w holds rows w*16*RT ..
     // w*16*RT + 16*RT - 1) for the Q^T operand and the softmax statistics.
@@ -337,30 +343,54 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_split_kernel(Params P) {
     // blocks have them in closed form: every query q0 .. min(q0 + QT, Q) - 1
     // of the tile has rows, and a row's frontier grows with its query.
     // Packed blocks reduce their descriptors over the workgroup.
+    // Packed blocks also mark which of the split's first 64 tiles hold a
+    // key that some row sees (bit i: tokens t_begin + TILE i ..): each
+    // query tile sees the prefix, the pending block and its own branches,
+    // not the other branches' keys, so most tiles past the prefix are
+    // skipped.  A skipped tile would add exactly nothing to any row's
+    // (m, l, O).
     int a_min = INT_MAX, w_end = 0;
+    uint64_t tile_vis = ~0ull;
     if constexpr (MODE == kPacked) {
         int amin = INT_MAX, wend = 0;
+        uint64_t tv = 0;
+        const int tb = s * P.split_tokens;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
             if (row_ok[rt]) {
                 amin = min(amin, va[rt]);
                 wend = max(wend, max(va[rt], vhi[rt]));
+                // keys below va: tiles [0, ceil((va - tb) / TILE));
+                // keys [vlo, vhi): tiles floor((vlo - tb) / TILE) .. ceil((vhi - tb) / TILE) - 1
+                tv |= bits_below(va[rt] > tb ? (va[rt] - tb + TILE - 1) / TILE : 0);
+                if (vlo[rt] < vhi[rt] && vhi[rt] > tb)
+                    tv |= bits_below((vhi[rt] - tb + TILE - 1) / TILE) &
+                          ~bits_below(vlo[rt] > tb ? (vlo[rt] - tb) / TILE : 0);
             }
+        uint32_t tv_lo = (uint32_t)tv, tv_hi = (uint32_t)(tv >> 32);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             amin = min(amin, __shfl_xor(amin, o, 64));
             wend = max(wend, __shfl_xor(wend, o, 64));
+            tv_lo |= (uint32_t)__shfl_xor((int)tv_lo, o, 64);
+            tv_hi |= (uint32_t)__shfl_xor((int)tv_hi, o, 64);
         }
         if (lane == 0) {
             s_lim[0][w] = amin;
             s_lim[1][w] = wend;
+            s_tiles[0][w] = tv_lo;
+            s_tiles[1][w] = tv_hi;
         }
         __syncthreads();
+        tv_lo = tv_hi = 0;
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
             a_min = min(a_min, s_lim[0][i]);
             w_end = max(w_end, s_lim[1][i]);
+            tv_lo |= s_tiles[0][i];
+            tv_hi |= s_tiles[1][i];
         }
+        tile_vis = ((uint64_t)tv_hi << 32) | tv_lo;
     } else if constexpr (MODE == kCausal) {
         a_min = min(ctx - P.Q + q0 + 1, ctx);
         w_end = max(0, min(ctx - P.Q + min(q0 + P.QT, P.Q), ctx));
@@ -566,30 +596,47 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_split_kernel(Params P) {
     // across the compute) measured batch-8 verify 35.4 -> 35.0 us and nothing
     // at batch 1 or end to end: the tile loop is bound by its dependency
     // chain, not by load latency.
+    // The first tile at or after t (a tile start) that some row sees;
+    // every tile for causal and bidirectional blocks, and past the 64
+    // tiles the packed mask covers.
+    auto next_tile = [&](int t) -> int {
+        if constexpr (MODE == kPacked) {
+            const int i = (t - t_begin) / TILE;
+            if (i < 64) {
+                const uint64_t m = tile_vis >> i;
+                return m ? t + TILE * (int)__builtin_ctzll(m) : t_begin + 64 * TILE;
+            }
+        }
+        return t;
+    };
     u32x4 regA[2 * TILE * 16 / NT];
     int okA = 0;
-    if (t_begin < t_end) fetch(t_begin, regA, okA);
+    int t0 = next_tile(t_begin);
+    if (t0 < t_end) fetch(t0, regA, okA);
     // Whole tiles on in-pool pages store without zeroing; the split's
     // partial last tile (and every tile of a split that names an
     // out-of-pool page) zeroes its dead rows.  Two loops rather than a
     // per-tile branch: with the branch inside one loop the compiler
     // waits for the next tile's loads before the first MFMA.
-    int t0 = t_begin;
     if (pages_ok) {
-        for (; t0 + TILE <= t_end; t0 += TILE) {
+        while (t0 + TILE <= t_end) {
             __syncthreads();
             store_tile<NT>(lds, regA, okA, true);
             __syncthreads();
-            if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
+            const int tn = next_tile(t0 + TILE);
+            if (tn < t_end) fetch(tn, regA, okA);
             compute(t0);
+            t0 = tn;
         }
     }
-    for (; t0 < t_end; t0 += TILE) {
+    while (t0 < t_end) {
         __syncthreads();
         store_tile<NT>(lds, regA, okA, false);
         __syncthreads();
-        if (t0 + TILE < t_end) fetch(t0 + TILE, regA, okA);
+        const int tn = next_tile(t0 + TILE);
+        if (tn < t_end) fetch(tn, regA, okA);
         compute(t0);
+        t0 = tn;
     }
 
     // Row sums: reduce the per-lane partials over the 4 lanes of a row.

@@ -207,6 +207,32 @@ def test_packed_block_matches_engine_mask(A, Hq, prefixes, ps):
     _check(out, ref)
 
 
+@pytest.mark.parametrize("prefixes,ps", [([560, 1024, 33, 2048], 16), ([600, 5], 16), ([300, 700], 256)])
+def test_packed_tile_skipping_is_exact(prefixes, ps):
+    """A query tile skips the key tiles none of its rows sees.  Making one row
+    in every 16 see every key forces those tiles in; every other row's output
+    must not change by a single bit (a fully masked tile adds exactly
+    nothing to a row's running max, sum and output)."""
+    K = 16
+    specs = _packed_specs(K, 1)
+    Q = K * (1 + len(specs))
+    lens = [p + Q for p in prefixes]
+    dev = torch.device("cuda:0")
+    kv = workloads.paged_kv(41, lens, Hkv=8, D=128, page_size=ps, device="cpu")
+    q = workloads.queries(43, len(lens), Q, Hq=16, D=128).to(dev)
+    args = (kv.k_cache.to(dev), kv.v_cache.to(dev), kv.context_lens.to(dev), kv.block_table.to(dev))
+    vis = att.packed_visibility(K, [n for n, _ in specs])
+    witness = vis.clone()
+    rows = list(range(0, Q, 16))
+    witness[rows] = torch.tensor([Q, 0, 0], dtype=torch.int32)
+    a = att.packed_block_attn(q, *args, vis.to(dev))
+    b = att.packed_block_attn(q, *args, witness.to(dev))
+    torch.cuda.synchronize()
+    keep = [i for i in range(Q) if i % 16]
+    assert torch.equal(a[:, keep], b[:, keep])
+    assert not torch.equal(a[:, rows], b[:, rows])  # the witnesses did see more
+
+
 def test_packed_recovery_descriptor_equals_bidirectional_block():
     """A visibility of {Q, 0, 0} on every row is the recovery mask (d3d_draft_block_attn)."""
     dev = torch.device("cuda:0")
