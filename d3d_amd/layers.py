@@ -69,16 +69,17 @@ def rows64_splits(N: int, K: int) -> int:
 def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
     """F.linear(x, weight) for bf16 x [M, K] and weight [N, K].
 
-    Blocks of at most 64 rows with N % 64 == 0 and K % 128 == 0 run
-    d3d_gemm_rows64 when its grid (N / 64 column tiles times the split
-    count) is one or two workgroups per CU; when it splits K the result is a
-    SplitProduct for add_rmsnorm or qk_rope_append to consume.  Other
-    shapes use F.linear (hipBLASLt).
+    Contiguous, 16-byte aligned blocks of at most 64 rows with N % 64 == 0
+    and K % 128 == 0 run d3d_gemm_rows64 when its grid (N / 64 column tiles
+    times the split count) is one or two workgroups per CU; when it splits K
+    the result is a SplitProduct for add_rmsnorm or qk_rope_append to
+    consume.  Other shapes use F.linear (hipBLASLt).
     """
     M, K = x.shape
     N = weight.shape[0]
     if (M > ROWS64 or N % 64 or K % 128 or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
-            or not x.is_contiguous() or not weight.is_contiguous()):
+            or not x.is_contiguous() or not weight.is_contiguous()
+            or x.data_ptr() % 16 or weight.data_ptr() % 16):  # the kernel's 16-byte row loads
         return F.linear(x, weight)
     dev = _lib.require_device(x, weight)
     lib = _lib.load()

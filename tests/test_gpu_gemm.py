@@ -139,3 +139,9 @@ def test_project_falls_back_beyond_64_rows_and_odd_shapes():
     assert torch.equal(ly.project(x3, w3), F.linear(x3, w3))
     x4, w4 = _operands(64, 2048, 6144, seed=8)  # 32 tiles x 8 splits
     assert isinstance(ly.project(x4, w4), ly.SplitProduct)
+    # a contiguous view 2 bytes off 16-byte alignment
+    buf = torch.empty(64 * 6144 + 1, dtype=BF, device=DEV)
+    x5 = buf[1:].view(64, 6144)
+    x5.copy_(x4)
+    y5 = ly.project(x5, w4)
+    assert isinstance(y5, torch.Tensor) and torch.equal(y5, F.linear(x5, w4))
