@@ -187,7 +187,8 @@ def _packed_specs(K: int, A: int):
 
 
 @pytest.mark.parametrize("A,Hq,prefixes,ps", [(1, 16, [1024, 517, 33, 2048], 16), (3, 16, [200, 95], 16),
-                                              (1, 32, [640, 1], 16), (1, 16, [300, 700], 256)])
+                                              (1, 32, [640, 1], 16), (1, 16, [300, 700], 256),
+                                              (1, 16, [900], 16), (3, 16, [1500], 16)])
 def test_packed_block_matches_engine_mask(A, Hq, prefixes, ps):
     """Packed draft attention against the fp64 oracle under Engine._mask."""
     K = 16
