@@ -177,8 +177,8 @@ def test_block_length_and_vocabulary_extremes(K, V, T):
 @pytest.mark.parametrize("T", [0.0, 1.0])
 def test_workspace_reuse_across_calls_and_shapes(T):
     """One cached workspace serves calls of different sizes in turn (the
-    stats launch resets the hand-off counters and flags each call):
-    every call agrees with the oracle."""
+    stats launch resets the hand-off records each call): every call agrees
+    with the oracle."""
     for B, V in ((8, 151936), (1, 4096), (3, 70000), (8, 151936), (2, 1000)):
         inp = workloads.accept_inputs(B * 7 + V % 13, B=B, K=15, V=V, temperature=T)
         got, t, d = _run(inp, T)
@@ -218,3 +218,46 @@ def test_cpu_tensors_are_rejected_loudly():
     with pytest.raises(RuntimeError, match="HIP device"):
         ss.accept_fused(inp.target, inp.draft, inp.tokens, uniforms=inp.uniforms,
                         resample_uniform=inp.resample_u)
+
+
+def test_graph_replays_match_eager_calls():
+    """The acceptance captured in a HIP graph (its workspace owned by the
+    graph) gives, on every replay over new inputs copied into the static
+    buffers, the eager call's outputs."""
+    from d3d_amd import _lib
+    dev = _dev()
+    B, K, V = 4, 15, 151936
+    sets = [workloads.accept_inputs(300 + i, B=B, K=K, V=V, device="cuda") for i in range(4)]
+    t = sets[0].target.clone()
+    d = sets[0].draft.clone()
+    tok = sets[0].tokens.clone()
+    u = sets[0].uniforms.clone()
+    ru = sets[0].resample_u.clone()
+
+    def body():
+        return ss.accept_fused(t, d, tok, temperature=1.0, uniforms=u, resample_uniform=ru)
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        body()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    owner: list = []
+    g = torch.cuda.CUDAGraph()
+    with _lib.capture_workspaces(owner), torch.cuda.graph(g):
+        out = body()
+    assert owner, "the captured acceptance asked for no workspace"
+    for rep in range(8):
+        src = sets[rep % len(sets)]
+        for dst, x in ((t, src.target), (d, src.draft), (tok, src.tokens), (u, src.uniforms),
+                       (ru, src.resample_u)):
+            dst.copy_(x)
+        g.replay()
+        torch.cuda.synchronize()
+        got = [x.clone() for x in out]
+        want = ss.accept_fused(src.target, src.draft, src.tokens, temperature=1.0, uniforms=src.uniforms,
+                               resample_uniform=src.resample_u)
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), rep
+    del g
