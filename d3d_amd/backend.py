@@ -156,7 +156,7 @@ class Runner:
         return block_inputs(self.kv, seqs, self.name, [s.prefix for s in seqs], Q, self.device, self.width)
 
     def _step(self, kind: str, B: int, Q: int, width: int, vis: Optional[torch.Tensor], k: int):
-        key = (kind, B, Q, width, k, None if vis is None else tuple(map(tuple, vis.tolist())))
+        key = (kind, B, Q, width, k, None if vis is None else (tuple(vis.shape), vis.numpy().tobytes()))
         step = self._steps.get(key)
         if step is None:
             if kind == "verify":

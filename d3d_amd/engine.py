@@ -30,8 +30,10 @@ list); its results equal Engine._accepted on the posterior.
 from __future__ import annotations
 
 import time
+from functools import lru_cache
 from typing import Dict, List, Optional, Sequence as Seq, Tuple
 
+import numpy as np
 import torch
 
 from .attention import packed_visibility
@@ -60,6 +62,13 @@ def branch_specs(K: int, A: int, current: List[int], top: List[List[int]], shall
     return out
 
 
+@lru_cache(maxsize=64)
+def _packed_visibility(K: int, accepted: Tuple[int, ...]) -> torch.Tensor:
+    """packed_visibility for one branch layout, built once (the engine
+    repeats a handful of layouts every step); callers only read it."""
+    return packed_visibility(K, accepted)
+
+
 class _Mask:
     """Engine._mask's builder (serving/engine.py:35-52).
 
@@ -83,7 +92,7 @@ class _Mask:
         acc = self._accepted()
         if acc is None:
             return torch.tensor([[Q, 0, 0]] * Q, dtype=torch.int32)
-        vis = packed_visibility(self.K, acc)
+        vis = _packed_visibility(self.K, tuple(acc))
         if vis.shape[0] != Q:
             raise ValueError("packed block length does not match the branch specs")
         return vis
@@ -220,21 +229,25 @@ class Engine:
         groups = [(part[off:off + self.micro], shallow)
                   for part, shallow in partitions for off in range(0, len(part), self.micro)]
         pending = []
+        ar = np.arange(K, dtype=np.int64)
         for group, shallow in groups:
             specs = [branch_specs(K, A, s.current, s.top, shallow, miss_anchors if shallow else A) for s in group]
-            Q = K + len(specs[0]) * K
-            ids = torch.full((len(group), Q), self.mask_id, dtype=torch.long)
-            pos = torch.empty_like(ids)
+            nb = len(specs[0])
+            Q = K + nb * K
+            # Row b: the current block at prefix..prefix+K-1, then branch j
+            # (n accepted, anchor a) at prefix+n.. with a in its first slot.
+            ids = np.full((len(group), Q), self.mask_id, dtype=np.int64)
+            pos = np.empty((len(group), Q), dtype=np.int64)
             for b, s in enumerate(group):
-                ids[b, :K] = torch.tensor(s.current)
-                pos[b, :K] = torch.arange(s.prefix, s.prefix + K)
-                for j, (n, a) in enumerate(specs[b]):
-                    start = K + j * K
+                ns = np.array([n for n, _ in specs[b]], dtype=np.int64)
+                ids[b, :K] = s.current
+                pos[b, :K] = s.prefix + ar
+                pos[b, K:] = (s.prefix + ns[:, None] + ar[None, :]).reshape(-1)
+                for j, (_, a) in enumerate(specs[b]):
                     if a is not None:
-                        ids[b, start] = a
-                    pos[b, start:start + K] = torch.arange(s.prefix + n, s.prefix + n + K)
-            top, greedy = self.draft.forward(group, ids, positions=pos, mask_builder=self._mask(specs), topk=A + 1,
-                                             host=True)
+                        ids[b, K + j * K] = a
+            top, greedy = self.draft.forward(group, torch.from_numpy(ids), positions=torch.from_numpy(pos),
+                                             mask_builder=self._mask(specs), topk=A + 1, host=True)
             pending.append((group, specs, top, greedy))
         return pending
 
