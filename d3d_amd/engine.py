@@ -18,6 +18,13 @@ same constructor, methods and result dictionary:
   ``concurrency``, prefill in groups of 4, EOS and length stops, page
   release and the leak checks.
 
+Keywords past the reference's (``device``, ``page_size``, ``mask_id``,
+``use_graphs``, ``tuned_gemms``) choose the device, the KV page size, the
+draft's mask id, whether steps replay HIP graphs, and whether the step's
+library GEMMs use the solution choices in gemm_tuned_gfx950.csv
+(gemm_tuning.enable: process-wide, and a no-op where the file's library
+versions or GPU do not match).
+
 The reference runs the target in another process on another GPU
 (serving/target_process.py) and exchanges token lists over a pipe; here
 both models are co-resident, each Runner on its own HIP stream (its own
@@ -36,6 +43,7 @@ from typing import Dict, List, Optional, Sequence as Seq, Tuple
 import numpy as np
 import torch
 
+from . import gemm_tuning
 from .attention import packed_visibility
 from .backend import MASK_ID, Runner, SamplingParams
 from .model import Sequence
@@ -120,7 +128,7 @@ class Engine:
     def __init__(self, target, draft, block_size: int = 16, anchor_num: int = 3, draft_microbatch: int = 4,
                  pages: int = 512, backup: str = "neural", seed: int = 42, fast_miss_anchors: int = 0,
                  draft_pages: Optional[int] = None, *, device: str = "cuda:0", page_size: int = 16,
-                 mask_id: int = MASK_ID, use_graphs: bool = True):
+                 mask_id: int = MASK_ID, use_graphs: bool = True, tuned_gemms: bool = True):
         if backup not in ("neural", "fast", "fast_legacy"):
             raise ValueError(backup)
         if anchor_num < 1:
@@ -138,6 +146,10 @@ class Engine:
         self.K, self.A, self.micro = block_size, anchor_num, draft_microbatch
         self.mask_id = mask_id
         self.device = torch.device(device)
+        # The step's library GEMMs (packed-predict projections, LM heads, the
+        # 64-row target qkv and gate-ups) on the shipped TunableOp choices;
+        # a process-wide torch setting, left on when the engine goes.
+        self.tuned_gemms = gemm_tuning.enable() if tuned_gemms else False
         self.target = Runner(target, self.device, pages=pages, page_size=page_size, seed=seed,
                              use_graphs=use_graphs)
         self.draft = Runner(draft, self.device, draft=True, pages=pages if draft_pages is None else draft_pages,

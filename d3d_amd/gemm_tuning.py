@@ -1,0 +1,142 @@
+"""Library-GEMM solution choices for the engine's fixed projection shapes.
+
+The projections that stay on the BLAS libraries (F.linear: the 1088-row
+packed-predict projections and LM head, the 64-row target qkv and gate-up
+and both LM heads) run whatever solution hipBLASLt's heuristic returns for
+the shape.  PyTorch's TunableOp times every hipBLASLt and rocBLAS solution
+of a shape (the heuristic's default among them) on rotating HBM-resident
+operands and keeps the fastest; ``tune`` does that for the engine's step
+shapes and writes the results file, ``enable`` makes torch use the file's
+choices (tuning itself stays off, so no shape is timed at run time and
+shapes the file does not list keep the default solution).
+
+The choice changes the solution, not the operation: outputs stay within the
+usual bf16 GEMM rounding of one another, not bit-equal across solutions.
+
+Run on the GPU the engine serves on (the file's validator lines pin the
+torch, HIP, hipBLASLt and rocBLAS versions and the gfx arch; ``enable``
+ignores a file that does not match)::
+
+    python -m d3d_amd.gemm_tuning [--out PATH] [--duration MS]
+"""
+from __future__ import annotations
+
+import argparse
+import sys
+import time
+import warnings
+from pathlib import Path
+from typing import Iterable, List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+RESULTS = Path(__file__).with_name("gemm_tuned_gfx950.csv")
+_enabled: Optional[Path] = None
+
+
+def step_gemm_shapes(target, draft, block: int = 16, batches: Iterable[int] = (1, 2, 3, 4),
+                     anchors: Iterable[int] = (1, 3)) -> List[Tuple[int, int, int]]:
+    """(M, N, K) of every library GEMM of an engine step, for the given
+    batch sizes and anchor counts: the target's verify and the draft's
+    recovery over ``block`` rows per request (the projections that
+    layers.project leaves to hipBLASLt, plus the LM heads), and the draft's
+    packed predict over ``block * (2 + A * (block - 1))`` rows per request
+    (every projection and the LM head).  Sorted, without repeats."""
+    from .layers import ROWS64, rows64_splits
+
+    def projections(s):
+        q, kv = s.heads * s.head_dim, s.kv_heads * s.head_dim
+        return [(q + 2 * kv, s.hidden), (s.hidden, q), (2 * s.mlp, s.hidden), (s.hidden, s.mlp),
+                (s.vocab, s.hidden)]
+
+    out = set()
+    for b in batches:
+        M = block * b
+        for s in (target, draft):
+            for N, K in projections(s):
+                if N == s.vocab or M > ROWS64 or not rows64_splits(N, K):
+                    out.add((M, N, K))
+        for A in anchors:
+            Mp = b * block * (2 + A * (block - 1))
+            out.update((Mp, N, K) for N, K in projections(draft))
+    return sorted(out)
+
+
+def enable(path: Path = RESULTS) -> bool:
+    """Use the solution choices in ``path`` for every matching torch GEMM of
+    this process (TunableOp on, tuning off).  Returns False, leaving torch's
+    defaults, when there is no GPU, no file, or the file was made with other
+    library versions or another GPU."""
+    global _enabled
+    path = Path(path)
+    if _enabled == path:
+        return True
+    if not torch.cuda.is_available() or not path.is_file():
+        return False
+    tun = torch.cuda.tunable
+    tun.enable(True)
+    tun.tuning_enable(False)
+    try:
+        ok = bool(tun.read_file(str(path)))
+    except Exception as exc:  # a malformed or foreign file
+        warnings.warn(f"GEMM tuning results {path} not loaded: {exc}")
+        ok = False
+    if not ok:
+        tun.enable(False)
+        return False
+    _enabled = path
+    return True
+
+
+def disable() -> None:
+    """Back to the libraries' default solutions."""
+    global _enabled
+    if torch.cuda.is_available():
+        torch.cuda.tunable.enable(False)
+    _enabled = None
+
+
+def tune(shapes: Sequence[Tuple[int, int, int]], out: Path = RESULTS, duration_ms: int = 150,
+         rotating_mb: int = 512, log=print) -> None:
+    """Tune F.linear(x [M, K], w [N, K]) in bf16 for each shape and write the
+    validators and results to ``out``."""
+    dev = torch.device("cuda:0")
+    tun = torch.cuda.tunable
+    tun.enable(True)
+    tun.tuning_enable(True)
+    tun.set_max_tuning_duration(duration_ms)
+    tun.set_rotating_buffer_size(rotating_mb)
+    # TunableOp writes its own copy at exit; keep it beside the real file.
+    tun.set_filename(str(Path(out).with_suffix(".session.csv")))
+    g = torch.Generator(device=dev).manual_seed(0)
+    for M, N, K in shapes:
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        F.linear(x, w)
+        torch.cuda.synchronize(dev)
+        log(f"tuned M={M} N={N} K={K} in {time.perf_counter() - t0:.1f} s")
+        del x, w
+        torch.cuda.empty_cache()
+    tun.tuning_enable(False)
+    lines = [f"Validator,{k},{v}" for k, v in tun.get_validators()]
+    lines += [f"{op},{params},{kernel},{ms}" for op, params, kernel, ms in sorted(tun.get_results())]
+    Path(out).write_text("\n".join(lines) + "\n")
+    log(f"wrote {len(lines)} lines to {out}")
+
+
+def main(argv=None) -> int:
+    from .model import D3D_1P7B, QWEN3_8B
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--out", type=Path, default=RESULTS)
+    ap.add_argument("--duration", type=int, default=150, help="tuning milliseconds per shape and solution set")
+    args = ap.parse_args(argv)
+    shapes = step_gemm_shapes(QWEN3_8B, D3D_1P7B)
+    print(f"{len(shapes)} shapes", flush=True)
+    tune(shapes, args.out, args.duration, log=lambda s: print(s, flush=True))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
