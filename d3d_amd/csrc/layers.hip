@@ -36,8 +36,26 @@ constexpr int HD = 128;  // head dim
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16, round to nearest even, on the convert unit (v_cvt_pk_bf16_f32,
+// two values per instruction): the bits f32_to_bf16_bits gives for every
+// input but NaN, which stays a NaN.  The kernels here are bound by their
+// VALU work, of which the rounding was the largest part.
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ __forceinline__ uint16_t bits1(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
-__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+__device__ __forceinline__ float rbf(float f) { return bf16_bits_to_f32(bits1(f)); }
+// Both values of a pair rounded to bf16 with one conversion.
+__device__ __forceinline__ void rbf2(float& a, float& b) {
+    const uint32_t p = pack2(a, b);
+    a = __uint_as_float(p << 16);
+    b = __uint_as_float(p & 0xffff0000u);
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -61,7 +79,7 @@ __device__ __forceinline__ u32x4 sum_parts8(const float* parts, int splits, size
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h)
-        o[h] = (uint32_t)f32_to_bf16_bits(a[2 * h]) | ((uint32_t)f32_to_bf16_bits(a[2 * h + 1]) << 16);
+        o[h] = pack2(a[2 * h], a[2 * h + 1]);
     return o;
 }
 
@@ -69,7 +87,7 @@ __device__ __forceinline__ u32x4 sum_parts8(const float* parts, int splits, size
 __device__ __forceinline__ uint16_t sum_parts1(const float* parts, int splits, size_t stride, size_t e) {
     float a = parts[e];
     for (int sp = 1; sp < splits; ++sp) a += parts[(size_t)sp * stride + e];
-    return f32_to_bf16_bits(a);
+    return bits1(a);
 }
 
 // One workgroup per row of H entries (H a multiple of 8).  One wave per row
@@ -109,7 +127,7 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
             v[j][2 * h] = lo;
             v[j][2 * h + 1] = hi;
             ss += lo * lo + hi * hi;
-            rs[h] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+            rs[h] = pack2(lo, hi);
         }
         if (PARTS || x) *reinterpret_cast<u32x4*>(residual + off) = rs;
     }
@@ -124,9 +142,9 @@ __global__ __launch_bounds__(NT) void add_rmsnorm_kernel(const uint16_t* __restr
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-            const float lo = rbf(v[j][2 * h] * rstd) * bf16_bits_to_f32(wv[h] & 0xffffu);
-            const float hi = rbf(v[j][2 * h + 1] * rstd) * bf16_bits_to_f32(wv[h] >> 16);
-            o[h] = (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+            float lo = v[j][2 * h] * rstd, hi = v[j][2 * h + 1] * rstd;
+            rbf2(lo, hi);
+            o[h] = pack2(lo * bf16_bits_to_f32(wv[h] & 0xffffu), hi * bf16_bits_to_f32(wv[h] >> 16));
         }
         *reinterpret_cast<u32x4*>(out + off) = o;
     }
@@ -178,15 +196,22 @@ __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
     const float f = (float)pos * inv_freq[lane];
     const float x0 = bf(a), x1 = bf(b);
     const float rstd = rsqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + eps);
-    const float y0 = rbf(rbf(x0 * rstd) * w0);
-    const float y1 = rbf(rbf(x1 * rstd) * w1);
+    float y0 = x0 * rstd, y1 = x1 * rstd;
+    rbf2(y0, y1);
+    y0 *= w0;
+    y1 *= w1;
+    rbf2(y0, y1);
     // cos / sin of this lane's frequency (entries lane and lane + 64).
     const float cs = cosf(f), sn = sinf(f);
     float o0, o1;
     if constexpr (DRAFT_ROPE) {
-        const float c = rbf(cs), s = rbf(sn);
-        o0 = rbf(rbf(y0 * c) + rbf(-y1 * s));
-        o1 = rbf(rbf(y1 * c) + rbf(y0 * s));
+        float c = cs, s = sn;
+        rbf2(c, s);
+        float p0 = y0 * c, p1 = -y1 * s, p2 = y1 * c, p3 = y0 * s;
+        rbf2(p0, p1);
+        rbf2(p2, p3);
+        o0 = p0 + p1;
+        o1 = p2 + p3;
     } else {
         o0 = y0 * cs - y1 * sn;
         o1 = y1 * cs + y0 * sn;
@@ -198,8 +223,9 @@ __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
         if (!store) return;
         dst = k_cache + ((size_t)slot * Hkv + (h - Hq)) * HD;
     }
-    dst[lane] = f32_to_bf16_bits(o0);
-    dst[lane + 64] = f32_to_bf16_bits(o1);
+    const uint32_t ob = pack2(o0, o1);
+    dst[lane] = (uint16_t)(ob & 0xffffu);
+    dst[lane + 64] = (uint16_t)(ob >> 16);
 }
 
 // out[t, i] = silu(gate[t, i]) * up[t, i] with gate_up = [gate | up] per row.
@@ -221,7 +247,7 @@ __global__ __launch_bounds__(NT) void silu_mul_kernel(const uint16_t* __restrict
             const float uv = bf16_bits_to_f32(k ? (u[h] >> 16) : (u[h] & 0xffffu));
             r[k] = gv / (1.0f + expf(-gv)) * uv;
         }
-        o[h] = (uint32_t)f32_to_bf16_bits(r[0]) | ((uint32_t)f32_to_bf16_bits(r[1]) << 16);
+        o[h] = pack2(r[0], r[1]);
     }
     *reinterpret_cast<u32x4*>(out + t * M + c * 8) = o;
 }

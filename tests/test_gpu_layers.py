@@ -123,11 +123,13 @@ def _rope_slack(y, pos, inv_freq, draft):
 
 
 @pytest.mark.parametrize("draft", [False, True])
-# 256 and more tokens take the several-heads-per-wave launch; 8 + 2 x 2 heads
-# leave a partly empty wave there.
-@pytest.mark.parametrize("Hq,Hkv,T", [(32, 8, 128), (16, 8, 16), (8, 2, 3), (32, 8, 300), (8, 2, 257)])
+# 8 + 2 x 2 heads leave a partly empty workgroup; 1088 is the packed draft
+# block of four requests.
+@pytest.mark.parametrize("Hq,Hkv,T", [(32, 8, 128), (16, 8, 16), (8, 2, 3), (32, 8, 300), (8, 2, 257),
+                                      (16, 8, 1088)])
 def test_qk_rope_append(draft, Hq, Hkv, T):
-    D, P, ps = 128, 32, 16
+    D, ps = 128, 16
+    P = max(32, -(-T // ps) + 4)
     g = torch.Generator().manual_seed(Hq * 131 + T + draft)
     qkv = (torch.randn(T, (Hq + 2 * Hkv) * D, generator=g) * 2).to(BF)
     pos = torch.randint(0, 40000, (T,), generator=g)
