@@ -22,7 +22,9 @@ ignores a file that does not match)::
 from __future__ import annotations
 
 import argparse
+import os
 import sys
+import tempfile
 import time
 import warnings
 from pathlib import Path
@@ -70,11 +72,11 @@ def enable(path: Path = RESULTS) -> bool:
     library versions or another GPU."""
     global _enabled
     path = Path(path)
-    if _enabled == path:
-        return True
     if not torch.cuda.is_available() or not path.is_file():
         return False
     tun = torch.cuda.tunable
+    if _enabled == path and tun.is_enabled() and not tun.tuning_is_enabled():
+        return True
     tun.enable(True)
     tun.tuning_enable(False)
     try:
@@ -107,8 +109,9 @@ def tune(shapes: Sequence[Tuple[int, int, int]], out: Path = RESULTS, duration_m
     tun.tuning_enable(True)
     tun.set_max_tuning_duration(duration_ms)
     tun.set_rotating_buffer_size(rotating_mb)
-    # TunableOp writes its own copy at exit; keep it beside the real file.
-    tun.set_filename(str(Path(out).with_suffix(".session.csv")))
+    # TunableOp also writes its own copy at process exit: keep that out of the
+    # package directory.
+    tun.set_filename(os.path.join(tempfile.gettempdir(), f"d3d_tunableop_{os.getpid()}.csv"))
     g = torch.Generator(device=dev).manual_seed(0)
     for M, N, K in shapes:
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
