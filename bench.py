@@ -402,7 +402,7 @@ def e2e_bench(dev, new_tokens: int, warm_tokens: int):
     batch 4, prompts of 512 random ids, greedy, 16-token blocks, 16-token pages."""
     from d3d_amd.engine import Engine
     from d3d_amd.model import D3D_1P7B, QWEN3_8B
-    eng = Engine(QWEN3_8B, D3D_1P7B, anchor_num=1, pages=64, seed=42)
+    eng = Engine(QWEN3_8B, D3D_1P7B, anchor_num=1, pages=64, seed=42, tuned_gemms=True)
     g = torch.Generator().manual_seed(9)
     prompts = torch.randint(0, 151936, (4, 512), generator=g).tolist()
     # The warm-up captures the block graphs at the timed run's page-table

@@ -260,7 +260,10 @@ __device__ __forceinline__ Decision decide(const Params& P, int b, bool writer) 
     }
     {
         const uint64_t rej = __ballot(tid < K && !acc);
-        const uint64_t bb = __ballot(badp);
+        // Greedy acceptance only compares a token with the argmax, so an
+        // out-of-range token is a plain mismatch there; the other modes
+        // index p and q by it and report the request instead.
+        const uint64_t bb = __ballot(M != kGreedy && badp);
         const int wv = tid / kWave;
         if ((tid & (kWave - 1)) == 0 && wv < 2) {
             s_bits[wv] = rej;

@@ -22,8 +22,9 @@ Keywords past the reference's (``device``, ``page_size``, ``mask_id``,
 ``use_graphs``, ``tuned_gemms``) choose the device, the KV page size, the
 draft's mask id, whether steps replay HIP graphs, and whether the step's
 library GEMMs use the solution choices in gemm_tuned_gfx950.csv
-(gemm_tuning.enable: process-wide, and a no-op where the file's library
-versions or GPU do not match).
+(``tuned_gemms=True``, off by default: gemm_tuning.enable turns on
+TunableOp, a process-wide torch switch, and ``close()`` turns it back; a
+no-op where the file's library versions or GPU do not match).
 
 The reference runs the target in another process on another GPU
 (serving/target_process.py) and exchanges token lists over a pipe; here
@@ -128,7 +129,7 @@ class Engine:
     def __init__(self, target, draft, block_size: int = 16, anchor_num: int = 3, draft_microbatch: int = 4,
                  pages: int = 512, backup: str = "neural", seed: int = 42, fast_miss_anchors: int = 0,
                  draft_pages: Optional[int] = None, *, device: str = "cuda:0", page_size: int = 16,
-                 mask_id: int = MASK_ID, use_graphs: bool = True, tuned_gemms: bool = True):
+                 mask_id: int = MASK_ID, use_graphs: bool = True, tuned_gemms: bool = False):
         if backup not in ("neural", "fast", "fast_legacy"):
             raise ValueError(backup)
         if anchor_num < 1:
@@ -146,9 +147,12 @@ class Engine:
         self.K, self.A, self.micro = block_size, anchor_num, draft_microbatch
         self.mask_id = mask_id
         self.device = torch.device(device)
-        # The step's library GEMMs (packed-predict projections, LM heads, the
-        # 64-row target qkv and gate-ups) on the shipped TunableOp choices;
-        # a process-wide torch setting, left on when the engine goes.
+        # tuned_gemms: the step's library GEMMs (packed-predict projections,
+        # LM heads, the 64-row target qkv and gate-ups) on the shipped
+        # TunableOp choices.  TunableOp is a process-wide torch switch that
+        # would also reach the caller's own GEMMs of those shapes, so it is
+        # opt-in, and close() puts the switches back as they were.
+        self._tunable_saved = gemm_tuning.state() if tuned_gemms else None
         self.tuned_gemms = gemm_tuning.enable() if tuned_gemms else False
         self.target = Runner(target, self.device, pages=pages, page_size=page_size, seed=seed,
                              use_graphs=use_graphs)
@@ -160,7 +164,13 @@ class Engine:
             raise ValueError(f"mask id {mask_id} outside the draft vocabulary")
 
     def close(self) -> None:
+        """Wait for both streams; undo the TunableOp switch ``tuned_gemms``
+        turned on."""
         torch.cuda.synchronize(self.device)
+        if self._tunable_saved is not None:
+            gemm_tuning.restore(self._tunable_saved)
+            self._tunable_saved = None
+            self.tuned_gemms = False
 
     # -- failure propagation ---------------------------------------------------
     def _drain(self) -> None:

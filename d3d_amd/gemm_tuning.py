@@ -91,6 +91,29 @@ def enable(path: Path = RESULTS) -> bool:
     return True
 
 
+def state() -> Tuple[bool, bool, Optional[Path]]:
+    """TunableOp's process-wide switches (enabled, tuning enabled) and the
+    results file ``enable`` loaded, for :func:`restore`."""
+    if not torch.cuda.is_available():
+        return (False, False, None)
+    tun = torch.cuda.tunable
+    return (bool(tun.is_enabled()), bool(tun.tuning_is_enabled()), _enabled)
+
+
+def restore(saved: Tuple[bool, bool, Optional[Path]]) -> None:
+    """Put TunableOp's switches back as :func:`state` recorded them.  The
+    solution choices ``enable`` read stay in torch's table but are used only
+    while TunableOp is on."""
+    global _enabled
+    if not torch.cuda.is_available():
+        return
+    on, tuning, path = saved
+    tun = torch.cuda.tunable
+    tun.enable(on)
+    tun.tuning_enable(tuning)
+    _enabled = path if on else None
+
+
 def disable() -> None:
     """Back to the libraries' default solutions."""
     global _enabled

@@ -36,6 +36,12 @@ class SplitProduct:
     parts: torch.Tensor
     splits: int
 
+    def __post_init__(self):
+        # The consumers read splits x M x N floats from parts: a leading
+        # dimension other than splits would send them past the allocation.
+        if self.parts.ndim != 3 or self.splits < 1 or self.parts.shape[0] != self.splits:
+            raise ValueError(f"split partials must be [splits={self.splits}, M, N], got {tuple(self.parts.shape)}")
+
     @property
     def shape(self):
         return self.parts.shape[1:]
@@ -153,6 +159,8 @@ def qk_rope_append(qkv: Product, positions: torch.Tensor, q_norm: torch.Tensor, 
     if split is not None:
         if split.parts.dtype != torch.float32 or not split.parts.is_contiguous():
             raise ValueError("split partials must be contiguous fp32")
+        if split.parts.shape[2] != (heads + 2 * kv_heads) * k_cache.shape[3]:
+            raise ValueError("qkv row width must be (heads + 2 kv_heads) * head_dim")
         qkv = split.parts[0]
     else:
         _bf16_rows(qkv, "qkv")

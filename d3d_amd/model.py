@@ -322,6 +322,7 @@ class BlockStep:
     def __init__(self, model: "Qwen3PagedModel", kv: PagedKV, B: int, Q: int, width: int, causal: bool,
                  post=None, use_graph: bool = True, q_vis: Optional[torch.Tensor] = None):
         dev = model.device
+        self.device = dev
         self.model, self.kv, self.causal, self.post, self.use_graph = model, kv, causal, post, use_graph
         self.q_vis = None if q_vis is None else q_vis.to(dev, torch.int32).contiguous()
         self.ids = torch.zeros(B, Q, dtype=torch.int64, device=dev)

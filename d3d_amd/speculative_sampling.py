@@ -35,14 +35,55 @@ class SpeculativeSampleResult:
     all_accepted: bool
 
 
+# Messages for the out_token sentinels, as the reference's checks word them:
+# an out-of-range draft token fails the gather of single/speculative_sampling.py
+# :50-54, and torch.multinomial (:71) rejects a distribution without mass.
+_SENTINEL_ERRORS = {
+    _lib.D3D_TOKEN_BAD_DRAFT: (ValueError, "draft token id outside the vocabulary"),
+    _lib.D3D_TOKEN_EMPTY_DISTRIBUTION: (RuntimeError, "invalid multinomial distribution (sum of probabilities <= 0)"),
+    _lib.D3D_TOKEN_TIMEOUT: (RuntimeError, "acceptance residual hand-off timed out"),
+}
+
+
+def _raise_for_token(token: int, request: Optional[int] = None) -> None:
+    err = _SENTINEL_ERRORS.get(int(token))
+    if err is None:
+        if token < 0:
+            raise RuntimeError(f"acceptance returned an unknown status {token}")
+        return
+    cls, msg = err
+    raise cls(msg if request is None else f"request {request}: {msg}")
+
+
 class AcceptOutput(NamedTuple):
-    """Device tensors written by one fused-acceptance launch."""
+    """Device tensors written by one fused-acceptance launch.
+
+    ``out_token`` holds a token id (>= 0) or, for a request whose draw could
+    not be made, a negative status: ``D3D_TOKEN_BAD_DRAFT`` (a draft token
+    outside [0, V)), ``D3D_TOKEN_EMPTY_DISTRIBUTION`` (no probability mass to
+    draw from) or ``D3D_TOKEN_TIMEOUT``.  ``valid`` is the per-request mask of
+    real tokens, computed on the device; :meth:`check` reads the tokens once
+    and raises the reference's error for the first bad request.
+    """
 
     accepted: torch.Tensor  # [B] int32, accepted draft tokens (0..K)
     accept_mask: torch.Tensor  # [B, K] bool, per-position decision
-    out_token: torch.Tensor  # [B] int64, correction or bonus token
+    out_token: torch.Tensor  # [B] int64, correction or bonus token, or a status < 0
     all_accepted: torch.Tensor  # [B] bool
     posterior: torch.Tensor  # [B, K+1] int64, argmax of every target row
+
+    @property
+    def valid(self) -> torch.Tensor:
+        """[B] bool on the device: the request's out_token is a token id."""
+        return self.out_token >= 0
+
+    def check(self) -> "AcceptOutput":
+        """Raise ValueError / RuntimeError if any request carries a status
+        instead of a token (one host synchronisation); returns self."""
+        for b, token in enumerate(self.out_token.tolist()):
+            if token < 0:
+                _raise_for_token(token, b if self.out_token.numel() > 1 else None)
+        return self
 
 
 def _prep(t: torch.Tensor) -> torch.Tensor:
@@ -137,7 +178,8 @@ def accept_fused_sparse(
     ``target`` [B, K+1, V] as in :func:`accept_fused`; the draft side is
     ``draft_token_ids`` / ``draft_token_probs`` [B, K, S] (S <= 1024), the
     proposal support of single/speculative_sampling.py:79-143.  Support ids
-    outside [0, V) carry no mass.  No host synchronisation.
+    outside [0, V) carry no mass.  No host synchronisation; statuses in
+    ``out_token`` as for :func:`accept_fused`.
     """
     if target.ndim != 3 or draft_tokens.ndim != 2:
         raise ValueError("expected draft_tokens [B,K] and target [B,K+1,V]")
@@ -184,12 +226,7 @@ def _to_result(out: AcceptOutput) -> SpeculativeSampleResult:
         [out.accepted[0].long(), out.out_token[0], out.all_accepted[0].long()]
     ).cpu().tolist()
     n, token, all_acc = packed
-    if token == _lib.D3D_TOKEN_BAD_DRAFT:
-        raise ValueError("draft token id outside the vocabulary")
-    if token == _lib.D3D_TOKEN_EMPTY_DISTRIBUTION:
-        raise RuntimeError("invalid multinomial distribution (sum of probabilities <= 0)")
-    if token == _lib.D3D_TOKEN_TIMEOUT:
-        raise RuntimeError("acceptance residual hand-off timed out")
+    _raise_for_token(token)
     return SpeculativeSampleResult(
         accepted_draft_tokens=int(n),
         correction_token=out.out_token[:1].clone(),

@@ -17,10 +17,12 @@ threads at once therefore serialise on their shared stream.
 
 Teardown: HIP objects this package creates -- the dedicated streams and the
 HIP graphs captured by model.BlockStep, with their workspaces -- are
-released by an interpreter-exit hook, in order (drain the devices, drop the
-graphs and their memory, destroy the streams), while the HIP runtime and
-any attached tool are still fully up, instead of being left to the
-runtime's own static destruction.
+released by an interpreter-exit hook, in order (drain the devices that hold
+them, drop the graphs and their memory, drop the per-stream workspaces,
+destroy the streams), while the HIP runtime and any attached tool are still
+fully up, instead of being left to the runtime's own static destruction.
+The hook is private: the streams it destroys are shared by every live
+Runner, so it runs only when nothing can launch on them again.
 """
 from __future__ import annotations
 
@@ -48,16 +50,30 @@ def register_graph_owner(owner) -> None:
 def _ensure_hook() -> None:
     global _hook_registered
     if not _hook_registered:
-        atexit.register(teardown)
+        atexit.register(_teardown)
         _hook_registered = True
 
 
-def teardown() -> None:
-    """Release captured graphs and destroy the dedicated streams (idempotent)."""
+def _used_devices() -> List[int]:
+    """Devices that hold a dedicated stream or a captured graph's owner."""
+    devs = {d for d, _ in _pool}
+    for owner in list(_graph_owners):
+        dev = getattr(owner, "device", None)
+        if dev is not None:
+            devs.add(torch.device(dev).index or 0)
+    return sorted(devs)
+
+
+def _teardown() -> None:
+    """Interpreter-exit hook (idempotent): release captured graphs, drop the
+    workspaces cached for the dedicated streams and destroy the streams.
+    Only the devices this package put streams or graphs on are drained, so
+    no context is opened on another GPU."""
     try:
         if not torch.cuda.is_initialized():
             return
-        for d in range(torch.cuda.device_count()):
+        devices = _used_devices()
+        for d in devices:
             torch.cuda.synchronize(d)
     except Exception:
         return
@@ -68,11 +84,16 @@ def teardown() -> None:
             pass
     _graph_owners.clear()
     try:
-        torch.cuda.synchronize()
+        for d in devices:
+            torch.cuda.synchronize(d)
     except Exception:
         pass
     _pool.clear()
     if _streams:
+        from . import _lib
+        doomed = set(_streams)
+        for k in [k for k in _lib._workspaces if k[1] in doomed]:
+            del _lib._workspaces[k]
         hip = _runtime()
         while _streams:
             handle = _streams.pop()

@@ -16,6 +16,14 @@ Mirrors the verifier process's "verify" command, single/eval_async_packed.py:
   temperature softmax (_sampling_probs, :134-139);
 * a block of one token (no draft tail) draws the correction from the last
   row (:143-150).
+
+Tokens that cannot be drawn come back from the kernels as negative statuses
+(an out-of-range draft token, a distribution without mass).  The reference's
+gather and torch.multinomial raise there, so ``verify_step`` checks the
+correction tokens by default and raises the same errors; ``check=False``
+keeps the step free of host synchronisation and leaves the statuses in
+``correction_token`` for the caller (``correction_token >= 0`` marks the
+valid requests).
 """
 from __future__ import annotations
 
@@ -40,11 +48,16 @@ def verify_step(target: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], bloc
                 draft_token_probs: Optional[torch.Tensor] = None, draft_logits: Optional[torch.Tensor] = None,
                 uniforms: Optional[torch.Tensor] = None, resample_uniform: Optional[torch.Tensor] = None,
                 generator: Optional[torch.Generator] = None, name: str = "target", width: Optional[int] = None,
-                return_logits: bool = False) -> VerifyResult:
-    """Verify B blocks [B, Q] against the target; no host synchronisation."""
+                return_logits: bool = False, check: bool = True) -> VerifyResult:
+    """Verify B blocks [B, Q] against the target.  With ``check`` (the
+    default) one host synchronisation reads the correction tokens and raises
+    ValueError / RuntimeError for a request that carries a status instead."""
     B, Q = blocks.shape
     dev = target.device
     blocks = blocks.to(dev, torch.int64).contiguous()
+    if check and bool(((blocks < 0) | (blocks >= target.shape.vocab)).any()):
+        # The embedding lookup of the forward must not see such an id.
+        raise ValueError("draft token id outside the vocabulary")
     for s in seqs:
         reserve(kv, s, name, s.prefix + Q)
     tables, slots, lens, logical, max_ctx = block_inputs(kv, seqs, name, [s.prefix for s in seqs], Q, dev, width)
@@ -58,6 +71,10 @@ def verify_step(target: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], bloc
         else:
             corr = sample_tokens(logits[:, -1], temperature, uniforms=resample_uniform, generator=generator)
         acc = torch.zeros(B, dtype=torch.int32, device=dev)
+        if check:
+            for b, token in enumerate(corr.tolist()):
+                if token < 0:
+                    ss._raise_for_token(token, b if B > 1 else None)
         return VerifyResult(posterior, acc, corr, logits if return_logits else None)
     tail = blocks[:, 1:]
     if greedy:
@@ -71,4 +88,6 @@ def verify_step(target: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], bloc
                               resample_uniform=resample_uniform, input_kind="logits", generator=generator)
     else:
         raise RuntimeError("temperature > 0 verification requires sparse draft q")
+    if check:
+        out.check()
     return VerifyResult(out.posterior, out.accepted, out.out_token, logits if return_logits else None)

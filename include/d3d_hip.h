@@ -51,7 +51,11 @@ extern "C" {
 
 /* Sentinels written to out_token[b] by the acceptance kernels. */
 #define D3D_TOKEN_EMPTY_DISTRIBUTION (-1) /* the resampling weights sum to zero */
-#define D3D_TOKEN_BAD_DRAFT (-2)          /* a draft token id lies outside [0, V) */
+/* A draft token id lies outside [0, V) (stochastic modes: the token indexes p
+ * and q; accepted = 0, all_accepted = 0 and the mask is 0 at bad positions).
+ * Greedy acceptance only compares tokens with the argmax, so there such a
+ * token is a mismatch and the request is decided as usual. */
+#define D3D_TOKEN_BAD_DRAFT (-2)
 /* The residual reduction's cross-workgroup wait (for the other parts of the
  * same request) did not end within its bound of over 100 ms.  Not expected:
  * workgroups are dispatched in order.  Every output but out_token is valid. */

@@ -27,6 +27,14 @@
  * such t, the last t with w_t > 0 is taken.  W <= 0 yields -1 (the reference
  * raises from torch.multinomial there).
  *
+ * A draft token outside [0, V) makes the reference's gather p[.., token_ids]
+ * (speculative_sampling.py:50-54, :108-110) raise: such a request reports
+ * out_token = -2 with accepted = 0 and all_accepted = 0; its mask holds the
+ * decision of every in-range position and 0 at the bad ones, and both
+ * margins are +inf (no rounding can change that outcome).  Greedy acceptance
+ * only compares tokens with the argmax (eval_sync.py:1223-1234), so there an
+ * out-of-range token is a mismatch like any other.
+ *
  * Each routine also reports its decision margins, which the fixture writer
  * uses to keep only inputs whose result does not depend on fp32 rounding:
  *   u_margin   = min_i |u_i - a_i| over every draft position
@@ -124,10 +132,15 @@ void oracle_accept_dense(const float* target, const float* draft, int kind, doub
     for (int b = 0; b < B; ++b) {
         const float* tb = target + (size_t)b * (K + 1) * V;
         const float* db = draft + (size_t)b * K * V;
-        int n = K;
+        int n = K, bad = 0;
         double um = INFINITY;
         for (int i = 0; i < K; ++i) {
             long tok = (long)tokens[(size_t)b * K + i];
+            if (tok < 0 || tok >= V) {
+                mask[(size_t)b * K + i] = 0;
+                bad = 1;
+                continue;
+            }
             oracle_row_probs(tb + (size_t)i * V, V, kind, T, p);
             oracle_row_probs(db + (size_t)i * V, V, kind, T, q);
             double a = accept_prob(p[tok], q[tok]);
@@ -137,6 +150,14 @@ void oracle_accept_dense(const float* target, const float* draft, int kind, doub
             double d = fabs(ui - a);
             if (d < um) um = d;
             if (!acc && n == K) n = i;
+        }
+        if (bad) {
+            accepted[b] = 0;
+            all_accepted[b] = 0;
+            out_token[b] = -2;
+            u_margin[b] = INFINITY;
+            cdf_margin[b] = INFINITY;
+            continue;
         }
         u_margin[b] = um;
         accepted[b] = n;
@@ -170,11 +191,16 @@ void oracle_accept_sparse(const float* target, int kind, double T, const int64_t
     double* p = (double*)malloc(sizeof(double) * (size_t)V);
     for (int b = 0; b < B; ++b) {
         const float* tb = target + (size_t)b * (K + 1) * V;
-        int n = K;
+        int n = K, bad = 0;
         double um = INFINITY;
         for (int i = 0; i < K; ++i) {
             size_t row = ((size_t)b * K + i) * S;
             long tok = (long)tokens[(size_t)b * K + i];
+            if (tok < 0 || tok >= V) {
+                mask[(size_t)b * K + i] = 0;
+                bad = 1;
+                continue;
+            }
             oracle_row_probs(tb + (size_t)i * V, V, kind, T, p);
             double qs = 0.0, qt = 0.0;
             for (int s = 0; s < S; ++s) qs += (double)q_probs[row + s];
@@ -188,6 +214,14 @@ void oracle_accept_sparse(const float* target, int kind, double T, const int64_t
             double d = fabs(ui - a);
             if (d < um) um = d;
             if (!acc && n == K) n = i;
+        }
+        if (bad) {
+            accepted[b] = 0;
+            all_accepted[b] = 0;
+            out_token[b] = -2;
+            u_margin[b] = INFINITY;
+            cdf_margin[b] = INFINITY;
+            continue;
         }
         u_margin[b] = um;
         accepted[b] = n;

@@ -93,3 +93,12 @@ def test_mask_to_visibility_rejects_other_shapes():
 def test_engine_rejects_bad_arguments_before_allocating(kw):
     with pytest.raises(ValueError):
         Engine("Qwen/Qwen3-8B", "fudan-generative-ai/D3D-1.7B-8B", **kw)
+
+
+def test_split_product_rejects_a_leading_dimension_other_than_splits():
+    from d3d_amd.layers import SplitProduct
+    ok = SplitProduct(torch.zeros(3, 4, 8), 3)
+    assert ok.shape == (4, 8)
+    for parts, splits in ((torch.zeros(2, 4, 8), 3), (torch.zeros(4, 8), 1), (torch.zeros(0, 4, 8), 0)):
+        with pytest.raises(ValueError, match="split partials must be"):
+            SplitProduct(parts, splits)

@@ -122,13 +122,21 @@ def test_equal_distributions_accept_all_and_draw_bonus_row():
 
 
 def test_bad_draft_token_is_reported_not_read():
+    """Stochastic modes index p and q by the draft token: an out-of-range
+    token reports the request (-2).  Greedy acceptance only compares the
+    token with the argmax (single/eval_sync.py:1223-1234): a mismatch."""
     inp = workloads.accept_inputs(5, B=3, K=4, V=512)
     inp.tokens[1, 2] = 512
     inp.tokens[2, 0] = -1
-    for T in (1.0, 0.0):
-        got, _, _ = _run(inp, T)
-        assert got["out_token"][1] == -2 and got["out_token"][2] == -2
-        assert got["out_token"][0] >= 0
+    got, _, _ = _run(inp, 1.0)
+    assert got["out_token"][1] == -2 and got["out_token"][2] == -2
+    assert got["out_token"][0] >= 0
+    got, t, _ = _run(inp, 0.0)
+    ref = oracle.accept_greedy(t.numpy(), inp.tokens.numpy())
+    for key in ("accepted", "out_token", "posterior"):
+        np.testing.assert_array_equal(got[key], ref[key])
+    np.testing.assert_array_equal(got["accept_mask"], ref["accept_mask"].astype(bool))
+    assert got["accepted"][2] == 0 and not got["accept_mask"][1][2]
 
 
 def test_empty_distribution_sentinel():
@@ -261,3 +269,62 @@ def test_graph_replays_match_eager_calls():
         for a, b in zip(got, want):
             assert torch.equal(a, b), rep
     del g
+
+
+def test_status_tokens_are_flagged_and_raise_on_check():
+    """A draft token outside the vocabulary (-2) and a request without
+    probability mass (-1) come back as statuses, flagged by ``valid`` on the
+    device, agreeing with the oracle, and ``check()`` raises the reference's
+    errors for them; a clean call checks through."""
+    from d3d_amd import _lib
+    dev = _dev()
+    V = 4096
+    inp = workloads.accept_inputs(21, B=3, K=15, V=V)
+    tokens = inp.tokens.clone()
+    tokens[1, 4] = V + 5
+    kw = dict(uniforms=inp.uniforms.to(dev), resample_uniform=inp.resample_u.to(dev))
+    out = ss.accept_fused(inp.target.to(dev), inp.draft.to(dev), tokens.to(dev), **kw)
+    assert out.valid.cpu().tolist() == [True, False, True]
+    assert int(out.out_token[1]) == _lib.D3D_TOKEN_BAD_DRAFT
+    ref = oracle.accept_dense(inp.target.numpy(), inp.draft.numpy(), tokens.numpy(), inp.uniforms.numpy(),
+                              inp.resample_u.numpy(), kind=oracle.KIND_LOGITS, temperature=1.0)
+    assert int(ref["out_token"][1]) == _lib.D3D_TOKEN_BAD_DRAFT
+    with pytest.raises(ValueError, match="request 1: draft token id outside the vocabulary"):
+        out.check()
+
+    p = torch.softmax(inp.target, -1)
+    q = torch.softmax(inp.draft, -1)
+    p[2] = 0.0  # request 2 has no target mass at all
+    out = ss.accept_fused(p.to(dev), q.to(dev), inp.tokens.to(dev), input_kind="probs", **kw)
+    assert out.valid.cpu().tolist() == [True, True, False]
+    ref = oracle.accept_dense(p.numpy(), q.numpy(), inp.tokens.numpy(), inp.uniforms.numpy(),
+                              inp.resample_u.numpy(), kind=oracle.KIND_PROBS)
+    assert int(out.out_token[2]) == int(ref["out_token"][2]) == _lib.D3D_TOKEN_EMPTY_DISTRIBUTION
+    with pytest.raises(RuntimeError, match="request 2: invalid multinomial distribution"):
+        out.check()
+
+    out = ss.accept_fused(inp.target.to(dev), inp.draft.to(dev), inp.tokens.to(dev), **kw)
+    assert out.check() is out and bool(out.valid.all())
+
+    # Greedy acceptance only compares tokens with the argmax: the same
+    # out-of-range token is a mismatch, decided as the oracle decides it.
+    out = ss.accept_fused(inp.target.to(dev), None, tokens.to(dev), temperature=0.0)
+    ref = oracle.accept_greedy(inp.target.numpy(), tokens.numpy())
+    assert out.check() is out
+    np.testing.assert_array_equal(out.accepted.cpu().numpy(), ref["accepted"])
+    np.testing.assert_array_equal(out.out_token.cpu().numpy(), ref["out_token"])
+    np.testing.assert_array_equal(out.accept_mask.cpu().numpy(), ref["accept_mask"].astype(bool))
+
+
+def test_sparse_status_tokens_raise_on_check():
+    from d3d_amd import _lib
+    dev = _dev()
+    inp = workloads.sparse_accept_inputs(22, B=2, K=15, V=4096, S=16)
+    tokens = inp.tokens.clone()
+    tokens[0, 0] = -7
+    out = ss.accept_fused_sparse(torch.softmax(inp.target, -1).to(dev), tokens.to(dev), inp.q_ids.to(dev),
+                                 inp.q_probs.to(dev), uniforms=inp.uniforms.to(dev),
+                                 resample_uniform=inp.resample_u.to(dev))
+    assert int(out.out_token[0]) == _lib.D3D_TOKEN_BAD_DRAFT and bool(out.valid[1])
+    with pytest.raises(ValueError, match="request 0: draft token id outside the vocabulary"):
+        out.check()

@@ -99,3 +99,37 @@ def test_sampled_verify_needs_a_proposal():
     model, kv, seqs, prompts, g = _setup(4, B=1)
     with pytest.raises(RuntimeError, match="requires sparse draft q"):
         verifier.verify_step(model, kv, seqs, torch.zeros(1, 16, dtype=torch.int64, device=DEV), temperature=1.0)
+
+
+def test_verify_step_rejects_out_of_vocabulary_draft_tokens():
+    """The check runs before the forward: the embedding never sees the id."""
+    model, kv, seqs, prompts, g = _setup(5, B=2)
+    blocks = torch.randint(0, 1000, (2, 16), generator=g)
+    blocks[1, 7] = 1000 + 3
+    with pytest.raises(ValueError, match="draft token id outside the vocabulary"):
+        verifier.verify_step(model, kv, seqs, blocks.to(DEV), temperature=0.9,
+                             draft_logits=torch.zeros(2, 15, 1000, device=DEV))
+
+
+def test_verify_step_raises_for_acceptance_statuses(monkeypatch):
+    """verify_step reads the acceptance's statuses: an empty distribution
+    (-1) raises the reference's multinomial error; with check=False the
+    status is handed back in correction_token."""
+    from d3d_amd import _lib
+    from d3d_amd import speculative_sampling as ss
+    real = ss.accept_fused
+
+    def with_status(*a, **k):
+        out = real(*a, **k)
+        out.out_token[1] = _lib.D3D_TOKEN_EMPTY_DISTRIBUTION
+        return out
+
+    monkeypatch.setattr(ss, "accept_fused", with_status)
+    model, kv, seqs, prompts, g = _setup(6, B=3)
+    blocks = torch.randint(0, 1000, (3, 16), generator=g).to(DEV)
+    dl = torch.randn(3, 15, 1000, generator=g).to(DEV)
+    with pytest.raises(RuntimeError, match="request 1: invalid multinomial distribution"):
+        verifier.verify_step(model, kv, seqs, blocks, temperature=0.9, draft_logits=dl)
+    res = verifier.verify_step(model, kv, seqs, blocks, temperature=0.9, draft_logits=dl, check=False)
+    assert int(res.correction_token[1]) == _lib.D3D_TOKEN_EMPTY_DISTRIBUTION
+    assert bool((res.correction_token[[0, 2]] >= 0).all())

@@ -228,6 +228,52 @@ def test_fp64_oracle_agrees_with_fp32_torch_restatement_at_full_vocab(seed):
     np.testing.assert_array_equal(out["accept_mask"][0].astype(bool), mask.numpy())
 
 
+def test_fp64_sparse_oracle_agrees_with_fp32_torch_sparse_restatement_at_full_vocab():
+    # torch_ref.verify_block_sparse restates single/speculative_sampling.py:79-143
+    # op for op in fp32; the fp64 C oracle computes the same decisions
+    # independently.  Seeds are kept only where both margins hold (the
+    # fixture margin policy), so the two roundings cannot disagree there; at
+    # least five of the first eight seeds qualify.
+    checked = 0
+    for seed in range(8):
+        inp = workloads.sparse_accept_inputs(seed, B=1, K=15, S=64)
+        p_t = torch_ref.sampling_probs(inp.target, 1.0)
+        out = oracle.accept_sparse(p_t.numpy(), inp.tokens.numpy(), inp.q_ids.numpy(), inp.q_probs.numpy(),
+                                   inp.uniforms.numpy(), inp.resample_u.numpy(), kind=oracle.KIND_PROBS)
+        if not (out["u_margin"][0] > 1e-5 and out["cdf_margin"][0] > 1e-6):
+            continue
+        n, tok, all_acc, mask = torch_ref.verify_block_sparse(inp.tokens, p_t, inp.q_ids, inp.q_probs,
+                                                              inp.uniforms, float(inp.resample_u[0]))
+        assert out["accepted"][0] == n, seed
+        assert out["out_token"][0] == tok, seed
+        assert bool(out["all_accepted"][0]) == all_acc, seed
+        np.testing.assert_array_equal(out["accept_mask"][0].astype(bool), mask.numpy())
+        checked += 1
+    assert checked >= 5
+
+
+def test_torch_sparse_restatement_known_answers():
+    # Residual path with a duplicate support id (scatter_add accumulates) and
+    # the all-accepted bonus path, worked by hand.
+    p = torch.tensor([[[0.5, 0.5, 0.0, 0.0], [0.0, 0.0, 0.0, 1.0]]])
+    ids = torch.tensor([[[1, 1, 2]]])
+    probs = torch.tensor([[[0.4, 0.4, 0.2]]])
+    # q(1) = 0.8, p(1) = 0.5: a = 0.625 < 0.7 rejects; residual [.5, 0, 0, 0]
+    n, tok, all_acc, mask = torch_ref.verify_block_sparse(torch.tensor([[1]]), p, ids, probs,
+                                                          torch.tensor([[0.7]]), 0.5)
+    assert (n, tok, all_acc, mask.tolist()) == (0, 0, False, [False])
+    # u = 0.6 <= 0.625 accepts; the bonus row is one-hot at 3
+    n, tok, all_acc, mask = torch_ref.verify_block_sparse(torch.tensor([[1]]), p, ids, probs,
+                                                          torch.tensor([[0.6]]), 0.5)
+    assert (n, tok, all_acc, mask.tolist()) == (1, 3, True, [True])
+    # q == p on the reject row: the residual mass is 0 and the draw falls back to p
+    probs_eq = torch.tensor([[[0.5, 0.5]]])
+    ids_eq = torch.tensor([[[0, 1]]])
+    n, tok, _, _ = torch_ref.verify_block_sparse(torch.tensor([[2]]), p, ids_eq, probs_eq,
+                                                 torch.tensor([[0.1]]), 0.75)
+    assert (n, tok) == (0, 1)  # token 2 has p = 0: rejected; p's CDF crosses 0.75 at id 1
+
+
 def test_confidence_topk_brute_force_and_ties():
     rng = np.random.default_rng(6)
     B, Q, V, mask_id = 3, 8, 40, 39
@@ -257,3 +303,26 @@ def test_transfer_schedule_closed_form():
     assert oracle.num_transfer_tokens(15, 4) == [4, 4, 4, 3]
     assert oracle.num_transfer_tokens(5, 3) == [2, 2, 1]
     assert oracle.num_transfer_tokens(3, 0) == [3]
+
+
+def test_out_of_range_draft_token_reports_the_request():
+    # The reference's gather p[.., token_ids] raises for such a token: the
+    # request is reported (-2), the mask keeps the in-range decisions.
+    p = [0.5, 0.5, 0, 0]
+    out = _one([p, p, p], [p, p], [0, 7], [0.3, 0.3], 0.5)
+    assert out["out_token"][0] == -2 and out["accepted"][0] == 0 and out["all_accepted"][0] == 0
+    assert list(out["accept_mask"][0]) == [1, 0]
+    assert out["u_margin"][0] == np.inf and out["cdf_margin"][0] == np.inf
+    out = _one([p, p, p], [p, p], [-1, 1], [0.3, 0.3], 0.5)
+    assert out["out_token"][0] == -2 and list(out["accept_mask"][0]) == [0, 1]
+    t = np.array([[p, p, p]], np.float32)
+    sp = oracle.accept_sparse(t, [[0, 4]], np.array([[[0, 1], [0, 1]]]), np.full((1, 2, 2), 0.5, np.float32),
+                              [[0.3, 0.3]], [0.5], kind=oracle.KIND_PROBS)
+    assert sp["out_token"][0] == -2 and list(sp["accept_mask"][0]) == [1, 0]
+
+
+def test_greedy_out_of_range_token_is_a_mismatch():
+    t = np.zeros((1, 3, 5), np.float32)
+    t[0, 0, 2] = t[0, 1, 3] = t[0, 2, 4] = 1.0
+    out = oracle.accept_greedy(t, [[2, 99]])
+    assert out["accepted"][0] == 1 and out["out_token"][0] == 3 and list(out["accept_mask"][0]) == [1, 0]

@@ -28,12 +28,12 @@ transformers = pytest.importorskip("transformers")
 SHAPE = ModelShape(layers=2, hidden=64, heads=4, kv_heads=2, head_dim=16, mlp=96, vocab=100)
 
 
-def _hf_model(seed: int):
+def _hf_model(seed: int, shape: ModelShape = SHAPE):
     from transformers import Qwen3Config, Qwen3ForCausalLM
-    cfg = Qwen3Config(vocab_size=SHAPE.vocab, hidden_size=SHAPE.hidden, intermediate_size=SHAPE.mlp,
-                      num_hidden_layers=SHAPE.layers, num_attention_heads=SHAPE.heads,
-                      num_key_value_heads=SHAPE.kv_heads, head_dim=SHAPE.head_dim, rope_theta=SHAPE.rope_theta,
-                      rms_norm_eps=SHAPE.eps, tie_word_embeddings=False, attention_bias=False,
+    cfg = Qwen3Config(vocab_size=shape.vocab, hidden_size=shape.hidden, intermediate_size=shape.mlp,
+                      num_hidden_layers=shape.layers, num_attention_heads=shape.heads,
+                      num_key_value_heads=shape.kv_heads, head_dim=shape.head_dim, rope_theta=shape.rope_theta,
+                      rms_norm_eps=shape.eps, tie_word_embeddings=False, attention_bias=False,
                       max_position_embeddings=1024)
     torch.manual_seed(seed)
     m = Qwen3ForCausalLM(cfg).eval()
@@ -47,13 +47,13 @@ def _hf_model(seed: int):
     return m
 
 
-def _weights(m):
+def _weights(m, shape: ModelShape = SHAPE):
     """The oracle's weight dict from the transformers module."""
     sd = {k: v.detach().float() for k, v in m.state_dict().items()}
-    d = SHAPE.head_dim
+    d = shape.head_dim
     half = d // 2
     layers = []
-    for i in range(SHAPE.layers):
+    for i in range(shape.layers):
         p = f"model.layers.{i}."
         layers.append(dict(
             qkv=torch.cat([sd[p + "self_attn.q_proj.weight"], sd[p + "self_attn.k_proj.weight"],
@@ -63,7 +63,7 @@ def _weights(m):
             down=sd[p + "mlp.down_proj.weight"],
             ln1=sd[p + "input_layernorm.weight"], ln2=sd[p + "post_attention_layernorm.weight"],
             qn=sd[p + "self_attn.q_norm.weight"], kn=sd[p + "self_attn.k_norm.weight"]))
-    inv_freq = 1.0 / (SHAPE.rope_theta ** (torch.arange(0, half, dtype=torch.float32) * 2 / d))
+    inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, half, dtype=torch.float32) * 2 / d))
     return dict(embed=sd["model.embed_tokens.weight"], norm=sd["model.norm.weight"], lm_head=sd["lm_head.weight"],
                 inv_freq=inv_freq, layers=layers)
 
@@ -82,6 +82,62 @@ def test_model_ref_matches_transformers_qwen3(prefix, block, bidirectional, shif
         got = model_ref.forward(W, SHAPE, ids, pos, mask)
     err = (got - ref).abs().max().item()
     assert err <= 2e-5 * max(ref.abs().max().item(), 1.0), err
+
+
+def _layer_step_logits(W, shape, ids_new, pos_new, past, mask_new):
+    """Chains model_ref.layer_step over every layer for the new rows, each
+    layer attending to its cached prefix keys/values ``past[l]``, then the
+    final norm and LM head."""
+    x, residual = W["embed"][ids_new], None
+    for L, (kp, vp) in zip(W["layers"], past):
+        x, residual = model_ref.layer_step(L, shape, W["inv_freq"], x, residual, pos_new, kp, vp, mask_new)
+    return model_ref._rms(residual + x, W["norm"], shape.eps) @ W["lm_head"].T
+
+
+@pytest.mark.parametrize("layers,prefix,block,shift", [(1, 9, 7, 0), (2, 24, 16, 37), (2, 1, 5, 3)])
+def test_layer_step_matches_transformers_with_cached_prefix(layers, prefix, block, shift):
+    """layer_step (the CPU-baseline workload) against transformers' Qwen3:
+    the prefix runs through transformers with its KV cache kept, the cache's
+    per-layer keys (after k_norm and RoPE) and values feed layer_step for the
+    new rows, and the chained result must equal transformers' logits of the
+    whole sequence on those rows (causal), and model_ref.forward's under the
+    prefix-causal + bidirectional-block mask."""
+    shape = ModelShape(layers=layers, hidden=64, heads=4, kv_heads=2, head_dim=16, mlp=96, vocab=100)
+    m = _hf_model(100 + prefix + block, shape)
+    W = _weights(m, shape)
+    T = prefix + block
+    ids = torch.randint(0, shape.vocab, (T,), generator=torch.Generator().manual_seed(T + 1))
+    pos = torch.arange(T) + shift
+    with torch.no_grad():
+        cache = m(ids[None, :prefix], position_ids=pos[None, :prefix], use_cache=True).past_key_values
+        past = [(c.keys[0].transpose(0, 1).float(), c.values[0].transpose(0, 1).float()) for c in cache.layers]
+        assert past[0][0].shape == (prefix, shape.kv_heads, shape.head_dim)
+        for bidirectional in (False, True):
+            mask = model_ref.causal_then_block(prefix, block, bidirectional)
+            got = _layer_step_logits(W, shape, ids[prefix:], pos[prefix:], past, mask[prefix:])
+            if bidirectional:
+                ref = model_ref.forward(W, shape, ids, pos, mask)[prefix:]
+            else:
+                ref = m(ids[None], position_ids=pos[None]).logits[0, prefix:]
+            err = (got - ref).abs().max().item()
+            assert err <= 2e-5 * max(ref.abs().max().item(), 1.0), (bidirectional, err)
+
+
+def test_layer_step_fails_with_a_shifted_cache():
+    """Negative control: prefix keys cached one position off must break the match."""
+    shape = ModelShape(layers=1, hidden=64, heads=4, kv_heads=2, head_dim=16, mlp=96, vocab=100)
+    m = _hf_model(11, shape)
+    W = _weights(m, shape)
+    prefix, block = 8, 6
+    ids = torch.arange(prefix + block) * 3 % shape.vocab
+    pos = torch.arange(prefix + block)
+    with torch.no_grad():
+        c = m(ids[None, :prefix], position_ids=pos[None, :prefix] + 1, use_cache=True).past_key_values.layers[0]
+        past = [(c.keys[0].transpose(0, 1).float(), c.values[0].transpose(0, 1).float())]
+        mask = model_ref.causal_then_block(prefix, block, False)[prefix:]
+        got = _layer_step_logits(W, shape, ids[prefix:], pos[prefix:], past, mask)
+        ref = m(ids[None], position_ids=pos[None]).logits[0, prefix:]
+    assert (got - ref).abs().max().item() > 1e-3
 
 
 def test_model_ref_fails_with_a_swapped_projection():
