@@ -31,6 +31,18 @@ memory-side cache; ``frac`` = algorithmic bytes / call duration / 8 TB/s:
   (17,563,648 B); confidence/top-k unmask over 4 x 16 bf16 rows
   (19,447,808 B).
 
+Attention rooflines also carry ``mfma_frac_of_peak`` (their TFLOP/s over
+the 2.5 PFLOP/s dense bf16 peak) and ``mfma_busy`` (the measured fraction of
+SIMD cycles the MFMA unit was busy, from rocprofv3 counters).
+``verify_step`` times configuration 1 as one step (the batch-1 verify
+attention, then the batch-1 acceptance); ``launch_floors`` what one kernel
+boundary and two dependent ones cost in the same graph harness.
+``draft_block_step_weights`` and ``engine_step_weights`` give the weight
+bytes those steps stream per call against the time they take.  ``value``
+times ``--steps`` new tokens per request (``config.new_tokens``); when that
+is not the configuration's 512, ``e2e_config_run`` reports the 512-token
+run beside it.
+
 ``roofline`` (the top-level object) is the batch-8 fused acceptance, the
 acceptance kernel at the size where its HBM efficiency is decided.
 ``cpu_baseline``: the fp32 torch-CPU restatement of one engine step, from
@@ -51,6 +63,8 @@ import time
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+CONFIG_NEW_TOKENS = 512  # new tokens per request of the engine-loop configuration
 
 # HBM bytes per call measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # (two passes of `bench.py --no-cpu-baseline --no-models --calibrate-copy`),
@@ -330,7 +344,9 @@ def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None):
            "us": round(ms * 1e3, 2), "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
            "frac": round(gbps / HBM_PEAK_GBPS, 4), "bar_frac": bar, "traffic": traffic}
     if flops is not None:
-        out["tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        tf = flops / (ms * 1e-3) / 1e12
+        out["tflops"] = round(tf, 1)
+        out["mfma_frac_of_peak"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
     return out
 
 
@@ -367,9 +383,77 @@ def kernel_rooflines(dev, calls: int):
                      r.flops))
     r, ms = run(lambda i: ConfStep(4, 16, 151936, 4, dev, seed=5 + i), 19_447_808)
     out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", r.bytes, ms, 0.70, TRAFFIC["c3_confidence"]))
+    # Configuration 1 as one step: the batch-1 block-verify attention, then
+    # the batch-1 fused acceptance (T = 1) over that step's 16 target and 15
+    # draft rows; algorithmic bytes are the two calls' sums.
+    r, ms = run(lambda i: PairStep(AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234 + i, num_pages=256),
+                                   acc(1, 1.0)(i)), 8_716_804 + 31 * 151936 * 4)
+    step = _roof(1, "verify step: block-verify attention (batch 1, prefix 2048) + fused acceptance (batch 1, T=1)",
+                 r.bytes, ms, None, None)
     del r
     torch.cuda.empty_cache()
+    return out, step
+
+
+class FillStep(_Bound):
+    """One (or ``n`` dependent) launches of torch's one-element fill kernel:
+    the cost of a kernel boundary in the graph harness, with no data."""
+
+    def __init__(self, dev, n: int):
+        self.t = torch.zeros(1, device=dev)
+        self.n = n
+        self.args = (None,)
+        self.bytes = 0
+
+    def __call__(self):
+        for _ in range(self.n):
+            self.t.zero_()
+
+
+class PairStep(_Bound):
+    """Two pre-bound calls run back to back on one stream."""
+
+    def __init__(self, a, b):
+        self.a, self.b = a, b
+        self.args = (None,)
+        self.bytes = a.bytes + b.bytes
+
+    def bind_stream(self, handle: int) -> None:
+        self.a.bind_stream(handle)
+        self.b.bind_stream(handle)
+
+    def __call__(self):
+        self.a()
+        self.b()
+
+
+def launch_floors(dev, calls: int):
+    """Per-call time of one kernel with no work and of two dependent ones,
+    replayed from the same 40-call graphs as the rooflines: what a one- or
+    two-launch call costs before it moves a byte."""
+    warm = max(calls // 10, 3)
+    out = {}
+    for n, key in ((1, "one_launch_us"), (2, "two_dependent_launches_us")):
+        r = Rotating(lambda i: FillStep(dev, n), 1, max_sets=2)
+        out[key] = round(time_graph(r, calls, warm, dev) * 1e3, 2)
+    out["kernel"] = "torch one-element fill (no data)"
     return out
+
+
+def weight_bytes(shape) -> int:
+    """bf16 weight bytes one forward streams: every decoder layer's
+    projections and norms, the final norm and the LM head (the embedding is
+    gathered row by row, not streamed)."""
+    h, d = shape.hidden, shape.head_dim
+    q, kv = shape.heads * d, shape.kv_heads * d
+    layer = (q + 2 * kv) * h + h * q + 2 * shape.mlp * h + h * shape.mlp + 2 * h + 2 * d
+    return 2 * (shape.layers * layer + h + shape.vocab * h)
+
+
+def _weight_stream(nbytes: int, ms: float, what: str) -> dict:
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "weight_bytes": int(nbytes), "ms": round(ms, 3), "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "what": what}
 
 
 def draft_block_bench(dev, reps: int = 20):
@@ -580,7 +664,8 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst
 
-    roofs = kernel_rooflines(dev, args.kernel_calls)
+    roofs, verify_step = kernel_rooflines(dev, args.kernel_calls)
+    floors = launch_floors(dev, args.kernel_calls)
     print(f"kernels timed ({len(roofs)})", file=sys.stderr, flush=True)
     gemms = gemm_rows64_bench(dev, args.kernel_calls)
     print("64-row projections timed", file=sys.stderr, flush=True)
@@ -612,14 +697,27 @@ def main():
         "roofline": {k: top[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")} | {
             "kernel": top["kernel"], "algorithmic_bytes": top["algorithmic_bytes"], "us": top["us"]},
         "rooflines": roofs,
+        "verify_step": verify_step,
+        "launch_floors": floors,
         "gemm_rows64": gemms,
     }
     if not args.no_models:
-        out["draft_block_step_ms"] = round(draft_block_bench(dev), 3)
+        from d3d_amd.model import D3D_1P7B, QWEN3_8B
+        dms = draft_block_bench(dev)
+        out["draft_block_step_ms"] = round(dms, 3)
+        # 4 denoise iterations, each a full draft forward.
+        out["draft_block_step_weights"] = _weight_stream(
+            4 * weight_bytes(D3D_1P7B), dms, "4 draft forwards (Qwen3-1.7B shapes) per block step")
         print("draft block step timed", file=sys.stderr, flush=True)
         res = e2e_bench(dev, args.steps, args.warmup)
         out["value"] = round(res["steps_per_s"], 2)
         out["ms_per_step"] = round(1e3 / res["steps_per_s"], 3)
+        out["config"]["new_tokens"] = args.steps
+        # Per step: one target forward (the verify) and two draft forwards
+        # (the packed prediction and the miss recovery).
+        out["engine_step_weights"] = _weight_stream(
+            weight_bytes(QWEN3_8B) + 2 * weight_bytes(D3D_1P7B), 1e3 / res["steps_per_s"],
+            "one Qwen3-8B-shaped target forward + two Qwen3-1.7B-shaped draft forwards per engine step")
         out["e2e"] = {
             "steps": res["steps"],
             "decode_s": round(res["decode_s"], 3),
@@ -628,9 +726,20 @@ def main():
             "draft_ms": round(res["draft_ms"], 3),
             "overlap_fraction": round(res["overlap_fraction"], 3),
             "timeline_ms": res["timeline"][:3],
-            "note": "random weights: drafts almost never match, so each step commits 1 token",
+            "note": "random weights: drafts almost never match, so each step commits 1 token; value and "
+                    "ms_per_step time the --steps new tokens per request",
         }
         print("engine loop timed", file=sys.stderr, flush=True)
+        if args.steps != CONFIG_NEW_TOKENS:
+            full = e2e_bench(dev, CONFIG_NEW_TOKENS, args.warmup)
+            out["e2e_config_run"] = {
+                "new_tokens": CONFIG_NEW_TOKENS, "steps": full["steps"],
+                "steps_per_s": round(full["steps_per_s"], 2), "ms_per_step": round(1e3 / full["steps_per_s"], 3),
+                "verify_ms": round(full["verify_ms"], 3), "draft_ms": round(full["draft_ms"], 3),
+                "overlap_fraction": round(full["overlap_fraction"], 3),
+                "note": "the configuration's full output length (contexts grow from 512 to 1024 tokens)",
+            }
+            print("engine loop timed at the configuration's output length", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_engine_step()
         out["cpu_baselines"] = cpu_baselines()

@@ -74,8 +74,11 @@ SIGNATURES = {
     "d3d_lmhead_workspace_bytes": (_SZ, [_I, _I64, _I]),
     "d3d_lmhead_topk": (_I, [_P, _P, _I, _I, _I64, _I, _I, _P, _P, _P, _SZ, _P]),
     "d3d_sample_workspace_bytes": (_SZ, [_I, _I64]),
-    "d3d_sample_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P]),
-    "d3d_softmax_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _SZ, _P]),
+    "d3d_sample_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "d3d_softmax_rows": (_I, [_P, _I, _I, _I64, _F, _P, _P, _P, _P, _P, _SZ, _P]),
+    "d3d_row_filter": (_I, [_P, _I, _I, _I64, _F, _I, _F, _P, _P, _P]),
+    "d3d_support_workspace_bytes": (_SZ, [_I, _I]),
+    "d3d_sample_support_wide": (_I, [_P, _I, _I, _I64, _F, _I, _F, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "d3d_sample_support": (_I, [_P, _P, _I, _I, _F, _F, _P, _P, _P, _P, _P]),
     "d3d_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "d3d_qk_rope_append": (

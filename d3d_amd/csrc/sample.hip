@@ -3,7 +3,9 @@
 // Reference behaviour (D3D repository):
 //   single/eval_sync.py:287-305  _sampling_probs: T <= 1e-5 is one-hot at
 //       the argmax, else softmax(logits / T); top-k keeps the entries at or
-//       above the k-th largest scaled logit (ties kept, :293-295)
+//       above the k-th largest scaled logit (ties kept, :293-295); top-p
+//       (:296-303) and wide top-k come as the per-row filter of
+//       d3d_row_filter (filter.hip)
 //   single/eval_sync.py:308-338  _sample_tokens / _sample_with_prob: the
 //       argmax (probability 1) or a multinomial draw and its probability
 //   single/eval_sync.py:341-367  _sample_with_sparse_probs: top-S support of
@@ -39,6 +41,8 @@ struct Params {
     int N, V, C;
     float T;
     const float* kth;   // [N] top-k floor (raw logit), or null
+    const float* zf;    // [N] filter floor on z = x / T, or null
+    const int32_t* zlim;  // [N] ids kept at z == zf[n]: e <= zlim[n]
     const float* u;     // [N]
     RowStat* stats;     // [N][C]
     int64_t* tok;       // [N]
@@ -61,6 +65,24 @@ __device__ __forceinline__ void apply_floor(const Params& P, int n, float (&x)[L
     }
 }
 
+// Row filter of d3d_row_filter (top-k and top-p of _sampling_probs,
+// single/eval_sync.py:292-303): entry e with z = x / T is kept iff
+// z > zf[n], or z == zf[n] and e <= zlim[n]; the others become -inf.  x[j*E +
+// k] holds entry first + j * stride + k.
+template <int DT, bool UNIT_T, int LT>
+__device__ __forceinline__ void apply_filter(const Params& P, int n, int first, int stride, float (&x)[LT]) {
+    if (!P.zf) return;
+    constexpr int E = Vec<DT>::E;
+    const float f = P.zf[n];
+    const int lim = P.zlim[n];
+#pragma unroll
+    for (int j = 0; j < LT; ++j) {
+        const int e = first + (j / E) * stride + (j % E);
+        const float z = UNIT_T ? x[j] : x[j] / P.T;
+        x[j] = (z > f || (z == f && e <= lim)) ? x[j] : -INFINITY;
+    }
+}
+
 template <int DT, bool VEC, Mode M, bool UNIT_T>
 __global__ __launch_bounds__(NT) void sample_stats_kernel(Params P) {
     constexpr int E = Vec<DT>::E;
@@ -71,7 +93,10 @@ __global__ __launch_bounds__(NT) void sample_stats_kernel(Params P) {
     const int first = c * kChunk + threadIdx.x * E;
     float x[L];
     load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
-    if constexpr (M != kGreedy) apply_floor<UNIT_T>(P, n, x);
+    if constexpr (M != kGreedy) {
+        apply_floor<UNIT_T>(P, n, x);
+        apply_filter<DT, UNIT_T>(P, n, first, NT * E, x);
+    }
     const RowStat st = chunk_stats<DT, M, UNIT_T>(x, first, P.T, M == kGreedy, rf, ri);
     if (threadIdx.x == 0) P.stats[(size_t)n * P.C + c] = st;
 }
@@ -155,6 +180,7 @@ __global__ __launch_bounds__(NT) void sample_pick_kernel(Params P) {
             float x[L];
             load_tile<DT, VEC, false, L>(row, P.V, first, NT * E, -INFINITY, x);
             apply_floor<UNIT_T>(P, n, x);
+            apply_filter<DT, UNIT_T>(P, n, first, NT * E, x);
             float run = 0.f;
             int found = INT_MAX, lastpos = -1;
 #pragma unroll
@@ -319,6 +345,7 @@ __global__ __launch_bounds__(NT) void softmax_write_kernel(Params P) {
         float x[L];
         load_tile<DT, VEC, true, L>(row, P.V, first, NT * E, -INFINITY, x);
         apply_floor<UNIT_T>(P, n, x);
+        apply_filter<DT, UNIT_T>(P, n, first, NT * E, x);
         const float Mrow = s_row[0], inv = s_row[1];
 #pragma unroll
         for (int j = 0; j < L / E; ++j)
@@ -359,8 +386,9 @@ extern "C" size_t d3d_sample_workspace_bytes(int N, int64_t V) {
 }
 
 extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
-                               const float* kth, const float* uniforms, int64_t* tokens_out, float* probs_out,
-                               void* workspace, size_t workspace_bytes, void* stream) {
+                               const float* kth, const float* zfloor, const int32_t* zlimit, const float* uniforms,
+                               int64_t* tokens_out, float* probs_out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
     using namespace sample;
     if (N < 0 || N > 65535 || V < 1 || V > (int64_t)rows::kMaxStatLds * rows::kChunk) return D3D_E_SHAPE;
     if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
@@ -375,6 +403,9 @@ extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, 
     P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
     P.T = greedy ? 1.0f : temperature;
     P.kth = greedy ? nullptr : kth;
+    if (!greedy && (zfloor == nullptr) != (zlimit == nullptr)) return D3D_E_NULL;
+    P.zf = greedy ? nullptr : zfloor;
+    P.zlim = greedy ? nullptr : zlimit;
     P.u = uniforms;
     P.stats = static_cast<rows::RowStat*>(workspace);
     P.tok = tokens_out;
@@ -394,8 +425,8 @@ extern "C" int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, 
 }
 
 extern "C" int d3d_softmax_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
-                                const float* kth, float* probs_out, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+                                const float* kth, const float* zfloor, const int32_t* zlimit, float* probs_out,
+                                void* workspace, size_t workspace_bytes, void* stream) {
     using namespace sample;
     if (N < 0 || N > 65535 || V < 1 || V > (int64_t)rows::kMaxStatLds * rows::kChunk) return D3D_E_SHAPE;
     if (dtype != D3D_DTYPE_F32 && dtype != D3D_DTYPE_BF16) return D3D_E_DTYPE;
@@ -410,6 +441,9 @@ extern "C" int d3d_softmax_rows(const void* logits, int dtype, int N, int64_t V,
     P.C = (int)((V + rows::kChunk - 1) / rows::kChunk);
     P.T = greedy ? 1.0f : temperature;
     P.kth = greedy ? nullptr : kth;
+    if (!greedy && (zfloor == nullptr) != (zlimit == nullptr)) return D3D_E_NULL;
+    P.zf = greedy ? nullptr : zfloor;
+    P.zlim = greedy ? nullptr : zlimit;
     P.u = nullptr;
     P.stats = static_cast<rows::RowStat*>(workspace);
     P.tok = nullptr;

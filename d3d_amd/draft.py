@@ -5,12 +5,13 @@ Mirrors single/eval_sync.py:
 * ``sampling_probs``           -- :287-305 (_sampling_probs), the dense
                                   proposal distribution: one-hot at T <= 1e-5,
                                   else softmax(logits / T) with the top-k
-                                  filter (ties with the k-th value kept)
+                                  filter (ties with the k-th value kept) and
+                                  the top-p (nucleus) filter
 * ``sample_tokens`` / ``sample_with_prob`` -- :308-338, proposal draws
                                   (argmax at T <= 1e-5, else the inverse CDF
                                   of the filtered softmax at a uniform)
-* ``sample_with_sparse_probs`` -- :341-367, top-S support, nucleus filter
-                                  and a draw from it
+* ``sample_with_sparse_probs`` -- :341-367, top-S support (any S, sorted
+                                  descending), nucleus filter and a draw
 * ``select_transfer``          -- :447-465 (_select_transfer) with
                                   caller-given tokens and confidences,
                                   "low_confidence" and "dynamic" remasking
@@ -110,23 +111,32 @@ def _uniforms(shape, dev, uniforms, generator):
     return uniforms.to(device=dev, dtype=torch.float32).reshape(shape).contiguous()
 
 
-def _kth(logits: torch.Tensor, top_k: int) -> Optional[torch.Tensor]:
-    """Per-row k-th largest logit (fp32, [N]) for the top-k filter, or None."""
-    if not top_k or top_k <= 0:
-        return None
+def _filters(logits: torch.Tensor, temperature: float, top_k: int, top_p: Optional[float]):
+    """The top-k / top-p filter of _sampling_probs (single/eval_sync.py:
+    292-303) for rows [N, V]: (kth, None, None) with kth the per-row k-th
+    largest logit for a top-k filter alone of at most 64 entries (one top-k
+    launch pair), (None, zfloor, zlimit) from d3d_row_filter for top-p or a
+    wider top-k, (None, None, None) when both are off."""
     V = logits.shape[-1]
-    k = min(int(top_k), V)
+    k = int(top_k) if top_k and top_k > 0 else 0
     if k >= V:
-        return None
-    if k > 64:
-        raise ValueError("top-k filtering supports top_k <= 64 (or top_k >= vocabulary size)")
-    _, vals = topk_tokens(logits, k, with_values=True)
-    return vals[..., k - 1].reshape(-1).contiguous()
-
-
-def _check_top_p(top_p: Optional[float]) -> None:
-    if top_p is not None and top_p < 1.0:
-        raise ValueError("top_p < 1 is supported for sparse proposals (return_sparse_proposal) only")
+        k = 0
+    p = 1.0 if top_p is None else float(top_p)
+    if not 0.0 < p <= 1.0:
+        raise ValueError("top_p must lie in (0, 1]")
+    if p >= 1.0 and k == 0:
+        return None, None, None
+    if p >= 1.0 and k <= 64:
+        _, vals = topk_tokens(logits, k, with_values=True)
+        return vals[..., k - 1].reshape(-1).contiguous(), None, None
+    N = logits.numel() // V
+    dev = logits.device
+    zf = torch.empty(N, dtype=torch.float32, device=dev)
+    lim = torch.empty(N, dtype=torch.int32, device=dev)
+    st = _lib.load().d3d_row_filter(logits.data_ptr(), _lib.dtype_code(logits), N, V, float(temperature), k, p,
+                                    zf.data_ptr(), lim.data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_row_filter")
+    return None, zf, lim
 
 
 def sample_with_prob(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0, *,
@@ -135,9 +145,10 @@ def sample_with_prob(logits: torch.Tensor, temperature: float = 0.0, top_k: int 
     """(tokens [...], probs [...]) of logits [..., V]: single/eval_sync.py:324-338.
 
     T <= 1e-5: the argmax with probability 1.  Otherwise the token is the
-    inverse-CDF draw of softmax(logits / T) -- over the entries at or above
-    the k-th largest when ``top_k`` > 0 -- at ``uniforms`` (one per row,
-    drawn with torch.rand when omitted) and probs its probability.
+    inverse-CDF draw of softmax(logits / T) over the entries the top-k and
+    top-p filters keep (both as in :func:`sampling_probs`) at ``uniforms``
+    (one per row, drawn with torch.rand when omitted) and probs its
+    probability.
     """
     dev = _lib.require_device(logits)
     lg = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
@@ -145,17 +156,15 @@ def sample_with_prob(logits: torch.Tensor, temperature: float = 0.0, top_k: int 
     V = lg.shape[-1]
     N = lg.numel() // V
     greedy = not temperature > 1e-5
-    if not greedy:
-        _check_top_p(top_p)
     u = None if greedy else _uniforms(lg.shape[:-1], dev, uniforms, generator)
-    kth = None if greedy else _kth(lg, top_k)
+    kth, zf, lim = (None, None, None) if greedy else _filters(lg, temperature, top_k, top_p)
     tok = torch.empty(lg.shape[:-1], dtype=torch.int64, device=dev)
     prob = torch.empty(lg.shape[:-1], dtype=torch.float32, device=dev)
     lib = _lib.load()
     ws = _lib.workspace(dev, "sample", lib.d3d_sample_workspace_bytes(max(N, 1), V))
     st = lib.d3d_sample_rows(lg.data_ptr(), _lib.dtype_code(lg), N, V, float(temperature), _lib.ptr(kth),
-                             _lib.ptr(u), tok.data_ptr(), prob.data_ptr(), ws.data_ptr(), ws.numel(),
-                             _lib.stream_ptr(dev))
+                             _lib.ptr(zf), _lib.ptr(lim), _lib.ptr(u), tok.data_ptr(), prob.data_ptr(),
+                             ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     _lib.check(st, "d3d_sample_rows")
     return tok, prob
 
@@ -169,22 +178,26 @@ def sample_tokens(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0
 
 def sampling_probs(logits: torch.Tensor, temperature: float = 0.0, top_k: int = 0,
                    top_p: float = 1.0) -> torch.Tensor:
-    """single/eval_sync.py:287-305: dense probabilities [..., V] fp32 (one-hot
-    at T <= 1e-5, else the top-k filtered softmax of logits / T)."""
+    """single/eval_sync.py:287-305: dense probabilities [..., V] fp32.
+
+    One-hot at the first argmax for T <= 1e-5.  Otherwise softmax over z =
+    logits / T restricted to the entries the filters keep: ``top_k`` > 0 the
+    entries at or above the k-th largest z (ties kept), then ``top_p`` < 1
+    the shortest prefix of those in descending order (ties by ascending id)
+    whose softmax mass exceeds top_p, the entry that crosses it included."""
     dev = _lib.require_device(logits)
     lg = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
     lg = lg.contiguous()
     V = lg.shape[-1]
     N = lg.numel() // V
     greedy = not temperature > 1e-5
-    if not greedy:
-        _check_top_p(top_p)
-    kth = None if greedy else _kth(lg, top_k)
+    kth, zf, lim = (None, None, None) if greedy else _filters(lg, temperature, top_k, top_p)
     out = torch.empty(lg.shape, dtype=torch.float32, device=dev)
     lib = _lib.load()
     ws = _lib.workspace(dev, "sample", lib.d3d_sample_workspace_bytes(max(N, 1), V))
     st = lib.d3d_softmax_rows(lg.data_ptr(), _lib.dtype_code(lg), N, V, float(temperature), _lib.ptr(kth),
-                              out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+                              _lib.ptr(zf), _lib.ptr(lim), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                              _lib.stream_ptr(dev))
     _lib.check(st, "d3d_softmax_rows")
     return out
 
@@ -194,13 +207,13 @@ def sample_with_sparse_probs(logits: torch.Tensor, temperature: float, top_k: in
     """(tokens, support ids [..., S], support probs [..., S]): single/eval_sync.py:341-367.
 
     T <= 1e-5: the argmax as a support of one with probability 1.  Otherwise
-    the support is the S = top_k largest logits (descending, ties by lower
-    id; 1 <= S <= 64), its probabilities softmax(logits / T) over the support
-    after the nucleus filter (``top_p`` < 1), and the token the inverse-CDF
-    draw from them.  ``top_k`` = 0 (the whole vocabulary) gives the support
-    in id order -- ids 0 .. V-1 with the dense softmax -- rather than sorted
-    by probability; acceptance against it is the same (the support's order
-    does not enter the acceptance arithmetic), and top_p < 1 then raises.
+    the support is the S = top_k largest z = logits / T (top_k = 0: the
+    whole vocabulary) in descending order, ties by ascending id; its
+    probabilities are softmax(z) over the support after the nucleus filter
+    (``top_p`` < 1: entry s > 0 is dropped when the mass of entries 0..s-1
+    exceeds top_p), and the token is the inverse-CDF draw from them in
+    support order.  Supports of up to 64 entries take the top-k kernel and
+    one wave per row; wider ones the sorted-support path.
     """
     dev = _lib.require_device(logits)
     if not temperature > 1e-5:
@@ -208,26 +221,31 @@ def sample_with_sparse_probs(logits: torch.Tensor, temperature: float, top_k: in
         return tok[..., 0], tok, torch.ones(tok.shape, dtype=torch.float32, device=dev)
     if not (top_p is None or 0.0 < top_p <= 1.0):
         raise ValueError("top_p must lie in (0, 1]")
+    p = float(1.0 if top_p is None else top_p)
     V = logits.shape[-1]
     S = int(top_k) if int(top_k) > 0 else V
     S = min(S, V)
-    if S == V and V > 64:
-        if top_p is not None and top_p < 1.0:
-            raise ValueError("top_p < 1 over the whole vocabulary (top_k=0) is not supported")
-        tok, _ = sample_with_prob(logits, temperature, uniforms=uniforms, generator=generator)
-        probs = sampling_probs(logits, temperature)
-        ids = torch.arange(V, device=dev).expand(probs.shape).contiguous()
+    lg = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
+    lg = lg.contiguous()
+    N = lg.numel() // V
+    u = _uniforms(lg.shape[:-1], dev, uniforms, generator)
+    tok = torch.empty(lg.shape[:-1], dtype=torch.int64, device=dev)
+    probs = torch.empty(*lg.shape[:-1], S, dtype=torch.float32, device=dev)
+    if S > 64:
+        ids = torch.empty(*lg.shape[:-1], S, dtype=torch.int64, device=dev)
+        lib = _lib.load()
+        nbytes = lib.d3d_support_workspace_bytes(max(N, 1), S)
+        if nbytes == 0:
+            raise RuntimeError("d3d_support_workspace_bytes failed")
+        ws = _lib.workspace(dev, "support", nbytes)
+        st = lib.d3d_sample_support_wide(lg.data_ptr(), _lib.dtype_code(lg), N, V, float(temperature), S, p,
+                                         u.data_ptr(), tok.data_ptr(), ids.data_ptr(), probs.data_ptr(), None,
+                                         ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
+        _lib.check(st, "d3d_sample_support_wide")
         return tok, ids, probs
-    if not 1 <= S <= 64:
-        raise ValueError("sparse proposals need 1 <= top_k <= 64 support entries (or top_k=0)")
-    ids, vals = topk_tokens(logits, S, with_values=True)
-    N = ids.numel() // S
-    u = _uniforms(logits.shape[:-1], dev, uniforms, generator)
-    tok = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev)
-    probs = torch.empty(ids.shape, dtype=torch.float32, device=dev)
-    st = _lib.load().d3d_sample_support(vals.data_ptr(), ids.data_ptr(), N, S, float(temperature),
-                                        float(1.0 if top_p is None else top_p), u.data_ptr(), tok.data_ptr(),
-                                        probs.data_ptr(), None, _lib.stream_ptr(dev))
+    ids, vals = topk_tokens(lg, S, with_values=True)
+    st = _lib.load().d3d_sample_support(vals.data_ptr(), ids.data_ptr(), N, S, float(temperature), p,
+                                        u.data_ptr(), tok.data_ptr(), probs.data_ptr(), None, _lib.stream_ptr(dev))
     _lib.check(st, "d3d_sample_support")
     return tok, ids, probs
 
@@ -420,8 +438,8 @@ def draft_block_step(drafter: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence]
     """
     if return_proposal not in (None, "logits", "probs", "sparse"):
         raise ValueError("return_proposal must be None, 'logits', 'probs' or 'sparse'")
-    if return_proposal == "logits" and top_k and top_k > 0:
-        raise ValueError("a logits proposal cannot carry the top-k filter: use 'probs' or 'sparse'")
+    if return_proposal == "logits" and ((top_k and top_k > 0) or (top_p is not None and top_p < 1.0)):
+        raise ValueError("a logits proposal cannot carry the top-k / top-p filters: use 'probs' or 'sparse'")
     cur = block.clone().contiguous()
     num_masks = _mask_count(cur, mask_id)
     if num_masks == 0:

@@ -357,16 +357,19 @@ size_t d3d_sample_workspace_bytes(int N, int64_t V);
  * row's k-th largest logit, so ties with it are kept), and token = the first
  * t with C_t > u[n] * W over the softmax weights, else the last t with
  * positive weight (inverse CDF in place of torch.multinomial); probs_out[n]
- * = p[token] (may be NULL).  N <= 65535.  D3D_TOKEN_EMPTY_DISTRIBUTION if a
- * row has no finite entry.
+ * = p[token] (may be NULL).  zfloor / zlimit [N] (both NULL, or both given:
+ * the row filter of d3d_row_filter) further restrict the entries to z >
+ * zfloor[n], or z == zfloor[n] at ids <= zlimit[n].  N <= 65535.
+ * D3D_TOKEN_EMPTY_DISTRIBUTION if a row has no finite entry.
  *
  * Replaces _sample_tokens / _sample_with_prob over _sampling_probs,
  * single/eval_sync.py:287-338 (top-k filtering :293-295; top-p is served by
  * d3d_sample_support).
  */
 int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float temperature,
-                    const float* kth, const float* uniforms, int64_t* tokens_out, float* probs_out,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    const float* kth, const float* zfloor, const int32_t* zlimit, const float* uniforms,
+                    int64_t* tokens_out, float* probs_out, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 /*
  * The dense proposal distribution of N logits rows [N, V]: probs_out [N, V]
@@ -379,7 +382,43 @@ int d3d_sample_rows(const void* logits, int dtype, int N, int64_t V, float tempe
  * keeps proposal_probs (:566-570, :577-584) for verify_speculative_block.
  */
 int d3d_softmax_rows(const void* logits, int dtype, int N, int64_t V, float temperature, const float* kth,
-                     float* probs_out, void* workspace, size_t workspace_bytes, void* stream);
+                     const float* zfloor, const int32_t* zlimit, float* probs_out, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/*
+ * The per-row filter of _sampling_probs' top-k and top-p options
+ * (single/eval_sync.py:292-303) over N logits rows [N, V] at temperature T >
+ * 1e-5, for d3d_sample_rows / d3d_softmax_rows: with z = logits / T (fp32),
+ * top_k in 1..V-1 keeps the entries at or above the k-th largest z (ties
+ * kept; 0 or >= V: off); top_p < 1 then sorts the kept entries by z
+ * descending (ties by ascending id), and keeps the shortest prefix whose
+ * softmax mass exceeds top_p (the entry that crosses it included).  The
+ * result is zfloor_out / zlimit_out [N]: entry e is kept iff z > zfloor, or
+ * z == zfloor and e <= zlimit.  NaN entries are never kept.  0 < top_p <= 1.
+ */
+int d3d_row_filter(const void* logits, int dtype, int N, int64_t V, float temperature, int top_k, float top_p,
+                   float* zfloor_out, int32_t* zlimit_out, void* stream);
+
+/* Bytes of workspace d3d_sample_support_wide needs. */
+size_t d3d_support_workspace_bytes(int N, int S);
+
+/*
+ * _sample_with_sparse_probs (single/eval_sync.py:341-367) for supports of
+ * any size 1 <= S <= V (V <= 2^18; S = V is top_k = 0, the whole vocabulary):
+ * support_ids_out [N, S] int64 = the S largest z = logits / T in descending
+ * order (ties by ascending id), support_probs_out [N, S] = softmax over the
+ * support after the nucleus filter (top_p < 1: entry s > 0 is dropped when
+ * the inclusive probability of entries 0..s-1 exceeds top_p, the rest
+ * renormalised), tokens_out [N] = the inverse-CDF draw over the support in
+ * support order at uniforms[n], token_probs_out [N] (may be NULL) its
+ * probability.  T > 1e-5, 0 < top_p <= 1.  Workspace:
+ * d3d_support_workspace_bytes(N, S).  d3d_topk_rows + d3d_sample_support
+ * cover S <= 64 in one launch pair.
+ */
+int d3d_sample_support_wide(const void* logits, int dtype, int N, int64_t V, float temperature, int S,
+                            float top_p, const float* uniforms, int64_t* tokens_out, int64_t* support_ids_out,
+                            float* support_probs_out, float* token_probs_out, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /*
  * Sparse proposal over a top-S support: support_vals / support_ids [N, S]

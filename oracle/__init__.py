@@ -196,24 +196,60 @@ def topk_keep(x, temperature: float, top_k: int) -> np.ndarray:
     return z >= kth
 
 
-def softmax_rows(logits, temperature: float, top_k: int = 0) -> np.ndarray:
-    """_sampling_probs (single/eval_sync.py:287-305) without top-p, fp64:
-    one-hot at the first argmax for T <= 1e-5, else softmax(x / T) over the
-    top-k kept entries, 0 elsewhere.  [N, V] -> [N, V]."""
+def filter_keep(x, temperature: float, top_k: int = 0, top_p: float = 1.0):
+    """The entries _sampling_probs keeps (single/eval_sync.py:292-303) on one
+    fp32 row, and the top-p decision margin.
+
+    z = x / T in fp32 (the reference's logits.float() / T).  Top-k keeps z >=
+    the k-th largest z (ties kept).  Top-p (< 1) orders the kept entries by z
+    descending -- ties by ascending id, the order of a stable sort -- takes
+    their fp64 softmax and its running sum c, and keeps entry j iff j == 0 or
+    c[j - 1] <= top_p (so the entry that first exceeds top_p stays).
+    Returns (keep [V] bool, margin): margin = min_j |c[j] - top_p| over the
+    sorted entries (inf when top-p is off), so a fixture whose margin exceeds
+    the kernels' rounding cannot be decided differently by them."""
+    x = _f32(x)
+    keep = topk_keep(x, temperature, top_k)
+    margin = np.inf
+    if top_p is not None and top_p < 1.0:
+        z = x / np.float32(temperature)
+        idx = np.flatnonzero(keep)
+        order = idx[np.lexsort((idx, -z[idx].astype(np.float64)))]
+        zz = z[order].astype(np.float64)
+        e = np.exp(zz - zz.max())
+        c = np.cumsum(e / e.sum())
+        margin = float(np.min(np.abs(c - top_p)))
+        before = np.concatenate([[0.0], c[:-1]])
+        drop = order[(before > top_p) & (np.arange(order.size) > 0)]
+        keep = keep.copy()
+        keep[drop] = False
+    return keep, margin
+
+
+def softmax_rows(logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
+    """_sampling_probs (single/eval_sync.py:287-305), fp64: one-hot at the
+    first argmax for T <= 1e-5, else softmax(x / T) over the entries
+    filter_keep keeps, 0 elsewhere.  [N, V] -> [N, V]."""
     x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
     out = np.zeros(x.shape, np.float64)
     for n in range(x.shape[0]):
         if temperature <= 1e-5:
             out[n, argmax(x[n])] = 1.0
             continue
-        keep = topk_keep(x[n], temperature, top_k)
+        keep, _ = filter_keep(x[n], temperature, top_k, top_p)
         z = x[n].astype(np.float64) / temperature
         e = np.where(keep, np.exp(z - z[keep].max()), 0.0)
         out[n] = e / e.sum()
     return out
 
 
-def sample_with_prob(logits, temperature: float, uniforms, top_k: int = 0):
+def filter_margins(logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
+    """filter_keep's top-p margin of every row of [N, V]."""
+    x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
+    return np.array([filter_keep(r, temperature, top_k, top_p)[1] for r in x])
+
+
+def sample_with_prob(logits, temperature: float, uniforms, top_k: int = 0, top_p: float = 1.0):
     """single/eval_sync.py:324-338 (_sample_with_prob over _sampling_probs),
     with torch.multinomial replaced by the inverse CDF of each row's fp64
     softmax at u[n] (over the top-k kept entries when top_k > 0).  Returns
@@ -226,7 +262,9 @@ def sample_with_prob(logits, temperature: float, uniforms, top_k: int = 0):
     prob = np.zeros(N, np.float64)
     margin = np.full(N, np.inf)
     for n in range(N):
-        p = softmax_rows(x[n][None], temperature, top_k)[0] if top_k else row_probs(x[n], KIND_LOGITS, temperature)
+        filtered = top_k or (top_p is not None and top_p < 1.0)
+        p = softmax_rows(x[n][None], temperature, top_k, top_p)[0] if filtered else row_probs(x[n], KIND_LOGITS,
+                                                                                                 temperature)
         if temperature <= 1e-5:
             tok[n] = int(np.argmax(p))
         else:
@@ -237,10 +275,12 @@ def sample_with_prob(logits, temperature: float, uniforms, top_k: int = 0):
 
 def sample_sparse(logits, temperature: float, S: int, uniforms, top_p: float = 1.0):
     """single/eval_sync.py:341-367 (_sample_with_sparse_probs), fp64: the S
-    largest entries of logits / T (descending, ties by lower id), softmax over
-    them, the nucleus filter (entry s > 0 dropped when the inclusive mass of
-    entries 0..s-1 exceeds top_p, then renormalised), inverse-CDF draw at
-    u[n].  Returns (tokens, ids [N,S], probs [N,S], margins)."""
+    largest entries of z = logits / T (z in fp32, the reference's
+    logits.float() / T; descending, ties by lower id), softmax over them, the
+    nucleus filter (entry s > 0 dropped when the inclusive mass of entries
+    0..s-1 exceeds top_p, then renormalised), inverse-CDF draw at u[n].
+    Returns (tokens, ids [N,S], probs [N,S], margins); the margin is the
+    draw's, and with top_p < 1 also the nucleus cut's (min |C_s - top_p|)."""
     x = _f32(logits).reshape(-1, np.asarray(logits).shape[-1])
     u = np.asarray(uniforms, np.float64).reshape(-1)
     N, V = x.shape
@@ -249,16 +289,20 @@ def sample_sparse(logits, temperature: float, S: int, uniforms, top_p: float = 1
     tok = np.zeros(N, np.int64)
     margin = np.zeros(N)
     for n in range(N):
-        z = x[n].astype(np.float64) / temperature
-        order = np.lexsort((np.arange(V), -z))[:S]
-        zs = z[order]
+        z32 = x[n] / np.float32(temperature)
+        order = np.lexsort((np.arange(V), -z32.astype(np.float64)))[:S]
+        zs = z32[order].astype(np.float64)
         e = np.exp(zs - zs.max())
         ids[n] = order
         probs[n] = e / e.sum()
+        cut = np.inf
         if top_p < 1.0:
-            before = np.concatenate([[0.0], np.cumsum(probs[n])[:-1]])
+            c = np.cumsum(probs[n])
+            cut = float(np.min(np.abs(c - top_p)))
+            before = np.concatenate([[0.0], c[:-1]])
             e = np.where(before > top_p, 0.0, e)
             probs[n] = e / e.sum()
         local, margin[n] = inverse_cdf(probs[n], u[n])
+        margin[n] = min(margin[n], cut)
         tok[n] = order[local]
     return tok, ids, probs, margin

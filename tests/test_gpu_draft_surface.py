@@ -218,15 +218,34 @@ def test_fused_commit_length_mismatch_raises():
                                         threshold=0.9, temperature=0.0, top_k=0, top_p=1.0, mask_id=MASK)
 
 
-@pytest.mark.parametrize("bad", [dict(remasking="random"), dict(top_p=0.9), dict(top_k=100)])
-def test_unsupported_parameters_raise(bad):
+def test_unsupported_parameters_raise():
     drafter = _drafter(26)
     block = torch.full((1, 16), MASK, dtype=torch.int64, device=DEV)
-    args = dict(remasking="low_confidence", threshold=0.9, temperature=1.0, top_k=0, top_p=1.0)
-    args.update(bad)
     with pytest.raises(ValueError):
-        dr.d3d_draft_block(drafter, block, 0, 2, args["remasking"], args["threshold"], args["temperature"],
-                           args["top_k"], args["top_p"], MASK, return_proposal_probs=True)
+        dr.d3d_draft_block(drafter, block, 0, 2, "random", 0.9, 1.0, 0, 1.0, MASK, return_proposal_probs=True)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 0.9), (100, 1.0), (100, 0.8)])
+def test_filtered_proposals_through_the_block_step(top_k, top_p):
+    """top-p and top-k above 64 (single/eval_sync.py:292-303) through the
+    reference's d3d_draft_block call: every position is unmasked, each
+    proposal row is a distribution, the drawn token carries probability
+    under it, and the filters cut the support (top_k: at least k entries, more
+    with ties; top_p: fewer than the whole vocabulary)."""
+    drafter = _drafter(27)
+    block = torch.full((1, 16), MASK, dtype=torch.int64, device=DEV)
+    torch.manual_seed(3)
+    out, probs = dr.d3d_draft_block(drafter, block, 0, 2, "low_confidence", 0.9, 1.0, top_k, top_p, MASK,
+                                    return_proposal_probs=True)
+    assert not bool((out == MASK).any())
+    p = probs[0].float()
+    np.testing.assert_allclose(p.sum(-1).cpu().numpy(), 1.0, rtol=1e-4)
+    picked = p.gather(-1, out[0][:, None])[:, 0]
+    assert bool((picked > 0).all())
+    support = (p > 0).sum(-1)
+    if top_k and top_p >= 1.0:
+        assert int(support.min()) >= top_k  # ties with the k-th value only add entries
+    assert int(support.max()) < p.shape[-1]
 
 
 def test_dynamic_remasking_one_hot_equals_low_confidence():

@@ -201,3 +201,73 @@ def test_dense_probs_vs_oracle(dtype):
         got = dr.sampling_probs(x.to(DEV), T)
         ref = oracle.softmax_rows(x.float().numpy(), T)
         np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=2e-5, atol=1e-9)
+
+
+TOP_P_MARGIN = 1e-6  # |C_j - top_p| the kernels' fp32 masses cannot decide the other way
+
+
+@pytest.mark.parametrize("V,top_k,top_p", [(151936, 0, 0.9), (151936, 0, 0.5), (151936, 1000, 0.8),
+                                           (5000, 100, 0.3), (151936, 70, 1.0), (5000, 4999, 1.0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_top_p_and_wide_top_k_vs_oracle(V, top_k, top_p, dtype):
+    """_sampling_probs' top-p filter and top-k filters wider than 64
+    (single/eval_sync.py:292-303): the kept set equals the oracle's exactly
+    (bf16 rows put many ties at the cut: the lowest ids stay), the dense
+    probabilities agree, and draws match on certified rows."""
+    N, T = 12, 0.8
+    x = _logits(V + top_k + int(100 * top_p), N, V, dtype)
+    u = torch.rand(N, generator=torch.Generator().manual_seed(top_k + 5))
+    dense = dr.sampling_probs(x.to(DEV), T, top_k, top_p)
+    tok, prob = dr.sample_with_prob(x.to(DEV), T, top_k, top_p, uniforms=u.to(DEV))
+    torch.cuda.synchronize()
+    xf = x.float().numpy()
+    rd = oracle.softmax_rows(xf, T, top_k, top_p)
+    fm = oracle.filter_margins(xf, T, top_k, top_p)
+    ok_f = fm > TOP_P_MARGIN
+    assert ok_f.mean() >= 0.5
+    got = dense.cpu().numpy()
+    np.testing.assert_array_equal((got > 0)[ok_f], (rd > 0)[ok_f])
+    np.testing.assert_allclose(got[ok_f], rd[ok_f], rtol=2e-5, atol=1e-8)
+    rt, rp, margin = oracle.sample_with_prob(xf, T, u.numpy(), top_k=top_k, top_p=top_p)
+    ok = ok_f & (margin > CDF_MARGIN)
+    assert ok.mean() >= 0.4
+    np.testing.assert_array_equal(tok.cpu().numpy()[ok], rt[ok])
+    np.testing.assert_allclose(prob.cpu().numpy()[ok], rp[ok], rtol=2e-5, atol=1e-9)
+
+
+def test_row_filter_tie_run_at_the_cut():
+    """Known answer: five equal logits after a leading one; top_p cuts inside
+    the run, so exactly the lowest ids of the run stay."""
+    x = torch.full((1, 300), -30.0)
+    x[0, 250] = 2.0
+    for i in (10, 20, 30, 40, 50):
+        x[0, i] = 1.0
+    p = np.exp(np.array([2.0] + [1.0] * 5) - 2.0)
+    p /= p.sum()
+    c = np.cumsum(p)
+    top_p = float((c[2] + c[3]) / 2)  # ids 250, 10, 20, 30 stay
+    dense = dr.sampling_probs(x.to(DEV), 1.0, 0, top_p).cpu()
+    assert torch.nonzero(dense[0] > 0)[:, 0].tolist() == [10, 20, 30, 250]
+
+
+@pytest.mark.parametrize("V,S,top_p", [(151936, 65, 1.0), (151936, 1000, 0.9), (5000, 4999, 1.0), (5000, 0, 0.7),
+                                       (151936, 0, 1.0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_wide_sparse_support_vs_oracle(V, S, top_p, dtype):
+    """_sample_with_sparse_probs with supports above 64 entries and top_k = 0
+    (the whole vocabulary; single/eval_sync.py:341-367): ids in descending
+    order of logits / T (ties by ascending id) bit-exact, probabilities after
+    the nucleus filter, draws on certified rows."""
+    N, T = 6, 0.8
+    x = _logits(V + S + 3, N, V, dtype)
+    u = torch.rand(N, generator=torch.Generator().manual_seed(S + 11))
+    tok, ids, probs = dr.sample_with_sparse_probs(x.to(DEV), T, S, top_p, uniforms=u.to(DEV))
+    torch.cuda.synchronize()
+    SS = S if S > 0 else V
+    assert ids.shape == (N, SS) and probs.shape == (N, SS)
+    rt, rids, rprobs, margin = oracle.sample_sparse(x.float().numpy(), T, SS, u.numpy(), top_p=top_p)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    ok = margin > CDF_MARGIN  # includes the nucleus cut's margin
+    assert ok.mean() >= 0.5
+    np.testing.assert_allclose(probs.cpu().numpy()[ok], rprobs[ok], rtol=2e-5, atol=1e-9)
+    np.testing.assert_array_equal(tok.cpu().numpy()[ok], rt[ok])

@@ -140,3 +140,69 @@ def test_transfer_schedule():
         for s in range(1, 9):
             sch = oracle.num_transfer_tokens(n, s)
             assert sum(sch) == n and max(sch) - min(sch) <= 1 and sch == sorted(sch, reverse=True)
+
+
+def test_top_p_filter_closed_form():
+    # probabilities 0.4 0.3 0.2 0.1: running sums 0.4 0.7 0.9 1.0
+    x = np.log(np.array([[0.1, 0.4, 0.2, 0.3]], np.float32))
+    np.testing.assert_allclose(oracle.softmax_rows(x, 1.0, top_p=0.5)[0], [0, 0.4 / 0.7, 0, 0.3 / 0.7], rtol=1e-6)
+    # 0.4 already exceeds 0.35: only the first entry stays
+    np.testing.assert_allclose(oracle.softmax_rows(x, 1.0, top_p=0.35)[0], [0, 1, 0, 0], rtol=1e-12)
+    np.testing.assert_allclose(oracle.softmax_rows(x, 1.0, top_p=0.75)[0], [0, 0.4 / 0.9, 0.2 / 0.9, 0.3 / 0.9],
+                               rtol=1e-6)
+    # top-k first: {0.4, 0.3} renormalised to 4/7, 3/7; 4/7 > 0.5 keeps one
+    np.testing.assert_allclose(oracle.softmax_rows(x, 1.0, top_k=2, top_p=0.5)[0], [0, 1, 0, 0], rtol=1e-12)
+    np.testing.assert_allclose(oracle.softmax_rows(x, 1.0, top_k=2, top_p=0.6)[0], [0, 4 / 7, 0, 3 / 7], rtol=1e-6)
+    keep, margin = oracle.filter_keep(x[0], 1.0, 0, 0.5)
+    assert keep.tolist() == [False, True, False, True]
+    np.testing.assert_allclose(margin, 0.1, rtol=1e-5)  # |0.4 - 0.5|
+    assert oracle.filter_keep(x[0], 1.0, 0, 1.0)[1] == np.inf
+
+
+def test_top_p_cut_through_ties_keeps_the_lowest_ids():
+    x = np.zeros(4, np.float32)  # four equal entries: running sums .25 .5 .75 1
+    keep, _ = oracle.filter_keep(x, 1.0, 0, 0.3)
+    assert keep.tolist() == [True, True, False, False]
+    x = np.array([2.0, 1.0, 1.0, 1.0, 3.0], np.float32)
+    p = np.exp(x - 3.0)
+    p /= p.sum()
+    # order: id 4, id 0, then ids 1, 2, 3 tied
+    c = np.cumsum(p[[4, 0, 1, 2, 3]])
+    top_p = (c[2] + c[3]) / 2  # between the 1st and 2nd tie: ids 4, 0, 1, 2 stay
+    keep, _ = oracle.filter_keep(x, 1.0, 0, float(top_p))
+    assert keep.tolist() == [True, True, True, False, True]
+
+
+def test_top_p_kept_set_is_the_minimal_sorted_prefix():
+    """Property pin: the kept set is a prefix of the descending order (ties
+    by id) whose mass exceeds top_p while the prefix without its last entry
+    does not (or it is everything), checked from the definitions in fp64."""
+    rng = np.random.default_rng(11)
+    for trial in range(60):
+        V = int(rng.integers(2, 400))
+        x = np.round(rng.normal(size=V) * 2, int(rng.integers(0, 3))).astype(np.float32)  # with ties
+        T = float(rng.choice([1.0, 0.7, 1.3]))
+        top_k = int(rng.choice([0, 1, 5, V // 2]))
+        top_p = float(rng.uniform(0.05, 0.99))
+        keep, _ = oracle.filter_keep(x, T, top_k, top_p)
+        base = oracle.topk_keep(x, T, top_k)
+        z = x / np.float32(T)
+        idx = np.flatnonzero(base)
+        order = sorted(idx, key=lambda i: (-float(z[i]), i))
+        kept = [i for i in order if keep[i]]
+        assert kept == order[:len(kept)] and len(kept) >= 1
+        assert not keep[~base].any()
+        e = np.exp(z[order].astype(np.float64) - float(z[order[0]]))
+        mass = np.cumsum(e / e.sum())
+        m = len(kept)
+        assert m == len(order) or mass[m - 1] > top_p
+        assert m == 1 or mass[m - 2] <= top_p
+
+
+def test_sample_sparse_ranks_the_fp32_quotient_with_ties_by_id():
+    T = np.float32(0.75)
+    a = np.float32(1.6)
+    b = np.nextafter(a, np.float32(2))  # equal fp32 quotients, different logits
+    x = np.array([[0.1, b, a, 0.0]], np.float32)
+    _, ids, _, _ = oracle.sample_sparse(x, float(T), 3, [0.5])
+    assert ids[0].tolist() == [1, 2, 0]
