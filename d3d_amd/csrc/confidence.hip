@@ -82,21 +82,62 @@ __device__ __forceinline__ int transfer_count(int k, int dynamic, int n_confiden
 // (may be null) records which positions were unmasked.  Rank of position i:
 // the number of masked positions with higher confidence, or equal
 // confidence and a lower index.
+//
+// Wave-parallel: each wave takes 64 candidate positions at a time, one per
+// lane, and walks the positions 64 at a time too: its lanes load 64 of them
+// (one each) and every candidate counts the ones ranked above it by reading
+// those 64 confidences and masks across lanes.  Q <= 64, the draft block's
+// size, is one step of each loop and one wave.
 __device__ __forceinline__ void rank_and_unmask(int64_t* block, int Q, int k, int n_masked, const uint8_t* mask,
                                                 const float* conf, const int* x0, uint8_t* selected) {
     const int kk = min(k, n_masked);
-    for (int i = threadIdx.x; i < Q; i += NT) {
-        bool pick = false;
-        if (mask[i]) {
-            const float ci = conf[i];
-            int rank = 0;
-            for (int j = 0; j < Q; ++j)
-                if (mask[j] && (conf[j] > ci || (conf[j] == ci && j < i))) ++rank;
-            pick = rank < kk;
-            if (pick) block[i] = x0[i];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+    for (int i0 = wv * kWave; i0 < Q; i0 += NT) {
+        const int i = i0 + lane;
+        const bool mi = i < Q && mask[i];
+        const float ci = i < Q ? conf[i] : 0.f;
+        int rank = 0;
+        for (int j0 = 0; j0 < Q; j0 += kWave) {
+            const int j = j0 + lane;
+            const bool mj = j < Q && mask[j];
+            const float cj = j < Q ? conf[j] : 0.f;
+            const int tn = min(kWave, Q - j0);  // the same for every lane
+#pragma unroll 16
+            for (int t = 0; t < tn; ++t) {
+                const float c = __shfl(cj, t, kWave);
+                const int m = __shfl((int)mj, t, kWave);
+                rank += m && (c > ci || (c == ci && j0 + t < i));
+            }
         }
-        if (selected) selected[i] = pick;
+        const bool pick = mi && rank < kk;
+        if (pick) block[i] = x0[i];
+        if (selected && i < Q) selected[i] = pick;
     }
+}
+
+// Masked positions and, of those, the ones whose confidence reaches the
+// threshold (for "dynamic" remasking), over the workgroup: one ballot per
+// wave and a fixed-order sum of the wave counts.
+__device__ __forceinline__ int2 count_masked(const uint8_t* mask, const float* conf, int Q, float threshold,
+                                             int2* s_w) {
+    int n = 0, nc = 0;
+    for (int i0 = 0; i0 < Q; i0 += NT) {
+        const int i = i0 + (int)threadIdx.x;
+        const bool m = i < Q && mask[i];
+        const bool c = m && conf[i] >= threshold;
+        n += __popcll(__ballot(m));
+        nc += __popcll(__ballot(c));
+    }
+    __syncthreads();
+    if ((threadIdx.x & (kWave - 1)) == 0) s_w[threadIdx.x / kWave] = make_int2(n, nc);
+    __syncthreads();
+    int2 t = make_int2(0, 0);
+#pragma unroll
+    for (int w = 0; w < NT / kWave; ++w) {
+        t.x += s_w[w].x;
+        t.y += s_w[w].y;
+    }
+    return t;
 }
 
 // Top-k unmask with caller-given tokens and confidences (the sampled draft
@@ -108,22 +149,16 @@ __global__ __launch_bounds__(NT) void select_transfer_kernel(int64_t* block, int
     __shared__ float sC[kMaxQ];
     __shared__ int sX[kMaxQ];
     __shared__ uint8_t sMask[kMaxQ];
-    __shared__ int s_masked, s_conf;
-    if (threadIdx.x == 0) s_masked = s_conf = 0;
-    __syncthreads();
-    int local = 0, lconf = 0;
+    __shared__ int2 s_w[NT / kWave];
     for (int i = threadIdx.x; i < Q; i += NT) {
         const size_t e = (size_t)b * Q + i;
         sMask[i] = block[e] == mask_id;
         sC[i] = conf[e];
         sX[i] = (int)x0[e];
-        local += sMask[i];
-        lconf += sMask[i] && sC[i] >= threshold;
     }
-    if (local) atomicAdd(&s_masked, local);  // LDS atomics
-    if (lconf) atomicAdd(&s_conf, lconf);
     __syncthreads();
-    rank_and_unmask(block + (size_t)b * Q, Q, transfer_count(k, dynamic, s_conf), s_masked, sMask, sC, sX,
+    const int2 cnt = count_masked(sMask, sC, Q, threshold, s_w);
+    rank_and_unmask(block + (size_t)b * Q, Q, transfer_count(k, dynamic, cnt.y), cnt.x, sMask, sC, sX,
                     selected ? selected + (size_t)b * Q : nullptr);
 }
 
@@ -134,11 +169,10 @@ __global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
     __shared__ float sM[kMaxQ], sS[kMaxQ];
     __shared__ int sArg[kMaxQ];
     __shared__ uint8_t sMask[kMaxQ];
-    __shared__ int s_masked;
+    __shared__ int2 s_w[NT / kWave];
 
     // Block ids are loaded before the merge so the load overlaps it.
     for (int i = threadIdx.x; i < Q; i += NT) sMask[i] = P.block[(size_t)b * Q + i] == P.mask_id;
-    if (threadIdx.x == 0) s_masked = 0;
     merge_row_stats<kLogits>(P.stats + (size_t)b * Q * P.C, Q, P.C, Q, sM, sS, sArg, lds);
     // The argmax entry's probability is exp(z_max - M) / S = 1 / S (1.0 in
     // one-hot mode).
@@ -149,18 +183,8 @@ __global__ __launch_bounds__(NT) void conf_select_kernel(Params P) {
         if (P.x0) P.x0[(size_t)b * Q + i] = sArg[i];
     }
     __syncthreads();
-    __shared__ int s_conf;
-    if (threadIdx.x == 0) {
-        int n = 0, nc = 0;
-        for (int i = 0; i < Q; ++i) {
-            n += sMask[i];
-            nc += sMask[i] && sS[i] >= P.threshold;
-        }
-        s_masked = n;
-        s_conf = nc;
-    }
-    __syncthreads();
-    rank_and_unmask(P.block + (size_t)b * Q, Q, transfer_count(P.k, P.dynamic, s_conf), s_masked, sMask, sS, sArg,
+    const int2 cnt = count_masked(sMask, sS, Q, P.threshold, s_w);
+    rank_and_unmask(P.block + (size_t)b * Q, Q, transfer_count(P.k, P.dynamic, cnt.y), cnt.x, sMask, sS, sArg,
                     nullptr);
 }
 
