@@ -82,6 +82,21 @@ TRAFFIC = {
 }
 
 
+# SQ_VALU_MFMA_BUSY_CYCLES per call (summed over the GPU's SIMDs), measured
+# with `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES GRBM_GUI_ACTIVE`
+# over `bench.py --no-models --no-cpu-baseline --kernel-calls 20`: the split
+# kernel's count (the combine issues no MFMA).  Each v_mfma_f32_16x16x32_bf16
+# counts 16 busy cycles.  mfma_busy = these cycles / (1024 SIMDs x 2.4 GHz x
+# the call's measured duration).
+MFMA_BUSY_CYCLES = {
+    "c1_verify_attn": 540_672,
+    "c2_verify_attn": 7_815_168,
+    "c3_draft_attn": 557_056,
+}
+SIMDS = 1024
+CLOCK_GHZ = 2.4
+
+
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -338,7 +353,7 @@ class Rotating:
         self.i = (self.i + 1) % len(self.calls)
 
 
-def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None):
+def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None, mfma_cycles=None):
     gbps = nbytes / (ms * 1e-3) / 1e9
     out = {"config": config, "kernel": kernel, "bound": "hbm", "algorithmic_bytes": int(nbytes),
            "us": round(ms * 1e3, 2), "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -347,6 +362,8 @@ def _roof(config, kernel, nbytes, ms, bar, traffic=None, flops=None):
         tf = flops / (ms * 1e-3) / 1e12
         out["tflops"] = round(tf, 1)
         out["mfma_frac_of_peak"] = round(tf / MFMA_BF16_PEAK_TFLOPS, 4)
+    if mfma_cycles is not None:
+        out["mfma_busy"] = round(mfma_cycles / (SIMDS * CLOCK_GHZ * 1e3 * ms * 1e3), 4)
     return out
 
 
@@ -371,16 +388,16 @@ def kernel_rooflines(dev, calls: int):
     out.append(_roof(0, "fused acceptance, batch 1, greedy", r.bytes, ms, 0.70, TRAFFIC["c0_accept_greedy"]))
     r, ms = run(lambda i: AttnStep([2048 + 16], 16, 32, 8, 16, True, dev, seed=1234 + i, num_pages=256), 8_716_804)
     out.append(_roof(1, "block-verify attention, batch 1, prefix 2048", r.bytes, ms, 0.60,
-                     TRAFFIC["c1_verify_attn"], r.flops))
+                     TRAFFIC["c1_verify_attn"], r.flops, MFMA_BUSY_CYCLES["c1_verify_attn"]))
     lens8 = [c + 16 for c in workloads.concurrent_context_lens(2024, B=8)]
     r, ms = run(lambda i: AttnStep(lens8, 16, 32, 8, 16, True, dev, seed=2024 + i), 126_471_608)
     out.append(_roof(2, f"block-verify attention, batch 8, contexts {lens8}", r.bytes, ms, 0.60,
-                     TRAFFIC["c2_verify_attn"], r.flops))
+                     TRAFFIC["c2_verify_attn"], r.flops, MFMA_BUSY_CYCLES["c2_verify_attn"]))
     r, ms = run(acc(8, 1.0), 248 * 151936 * 4)
     out.append(_roof(2, "fused acceptance, batch 8, T=1", r.bytes, ms, 0.70, TRAFFIC["c2_accept_b8"]))
     r, ms = run(lambda i: AttnStep([1024 + 16] * 4, 16, 16, 8, 16, False, dev, seed=77 + i), 17_564_688)
     out.append(_roof(3, "draft block attention, batch 4, prefix 1024", r.bytes, ms, 0.60, TRAFFIC["c3_draft_attn"],
-                     r.flops))
+                     r.flops, MFMA_BUSY_CYCLES["c3_draft_attn"]))
     r, ms = run(lambda i: ConfStep(4, 16, 151936, 4, dev, seed=5 + i), 19_447_808)
     out.append(_roof(3, "confidence / top-k unmask, 4 x 16 bf16 rows", r.bytes, ms, 0.70, TRAFFIC["c3_confidence"]))
     # Configuration 1 as one step: the batch-1 block-verify attention, then
