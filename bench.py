@@ -137,7 +137,11 @@ class AcceptStep(_Bound):
         self.mask = torch.empty(B, K, dtype=torch.uint8, device=dev)
         self.tokout = torch.empty(B, dtype=torch.int64, device=dev)
         self.alla = torch.empty(B, dtype=torch.uint8, device=dev)
-        self.post = torch.empty(B, K1, dtype=torch.int64, device=dev)
+        # The outputs are the accepted length, the mask and the token; the
+        # posterior (argmax of every target row) is asked for only where the
+        # decision is made of it (greedy).
+        self.greedy = temperature <= 1e-5
+        self.post = torch.empty(B, K1, dtype=torch.int64, device=dev) if self.greedy else None
         n = self.lib.d3d_accept_workspace_bytes(B, K, V)
         self.ws = torch.zeros(n, dtype=torch.uint8, device=dev)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
@@ -145,9 +149,8 @@ class AcceptStep(_Bound):
             self.t.data_ptr(), self.d.data_ptr(), _lib.D3D_DTYPE_F32, _lib.D3D_INPUT_LOGITS,
             self.tok.data_ptr(), self.u.data_ptr(), self.ru.data_ptr(), float(temperature), B, K, V,
             self.acc.data_ptr(), self.mask.data_ptr(), self.tokout.data_ptr(), self.alla.data_ptr(),
-            self.post.data_ptr(), self.ws.data_ptr(), n, self.stream,
+            None if self.post is None else self.post.data_ptr(), self.ws.data_ptr(), n, self.stream,
         )
-        self.greedy = temperature <= 1e-5
         self._check = _lib.check
         rows = B * (K + 1) + (0 if self.greedy else B * K)
         self.bytes = rows * V * 4

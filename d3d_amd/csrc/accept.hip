@@ -154,7 +154,10 @@ __global__ __launch_bounds__(NT) void accept_stats_kernel(Params P) {
     const int first = c * kChunk + threadIdx.x * E;
     float x[L];
     load_tile<DT, VEC, true, L>(row, V, first, NT * E, fill_value<M>(), x);
-    const bool want_arg = r <= K;  // posterior needs target rows only
+    // Argmax of the target rows: the greedy decision, and the posterior
+    // output when the caller asks for it (it costs the stats pass about 1 us
+    // at batch 8; the stochastic decision does not need it).
+    const bool want_arg = r <= K && (M == kGreedy || P.posterior != nullptr);
     const RowStat st = P.T == 1.0f ? chunk_stats<DT, M, true>(x, first, P.T, want_arg, rf, ri)
                                    : chunk_stats<DT, M, false>(x, first, P.T, want_arg, rf, ri);
     if (threadIdx.x == 0) {

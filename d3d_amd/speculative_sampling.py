@@ -70,7 +70,7 @@ class AcceptOutput(NamedTuple):
     accept_mask: torch.Tensor  # [B, K] bool, per-position decision
     out_token: torch.Tensor  # [B] int64, correction or bonus token, or a status < 0
     all_accepted: torch.Tensor  # [B] bool
-    posterior: torch.Tensor  # [B, K+1] int64, argmax of every target row
+    posterior: Optional[torch.Tensor]  # [B, K+1] int64, argmax of every target row; None if not asked for
 
     @property
     def valid(self) -> torch.Tensor:
@@ -92,10 +92,10 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
-def _outputs(B: int, K: int, dev: torch.device):
+def _outputs(B: int, K: int, dev: torch.device, posterior: bool = True):
     return (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, K, dtype=torch.uint8, device=dev),
             torch.empty(B, dtype=torch.int64, device=dev), torch.empty(B, dtype=torch.uint8, device=dev),
-            torch.empty(B, K + 1, dtype=torch.int64, device=dev))
+            torch.empty(B, K + 1, dtype=torch.int64, device=dev) if posterior else None)
 
 
 def accept_fused(
@@ -108,6 +108,7 @@ def accept_fused(
     resample_uniform: Optional[torch.Tensor] = None,
     input_kind: str = "logits",
     generator: Optional[torch.Generator] = None,
+    posterior: bool = True,
 ) -> AcceptOutput:
     """Batched fused acceptance: B requests of K draft tokens, one launch.
 
@@ -117,6 +118,9 @@ def accept_fused(
     is greedy acceptance, single/eval_sync.py:1223-1234, and ignores draft and
     uniforms) or probabilities (``input_kind="probs"``, normalised by their sum
     as at single/speculative_sampling.py:37-40).  No host synchronisation.
+    ``posterior=False`` leaves out the argmax of the target rows
+    (``AcceptOutput.posterior`` is None) for a caller that does not use it;
+    greedy acceptance computes it regardless, since its decision is made of it.
     """
     if target.ndim != 3 or draft_tokens.ndim != 2:
         raise ValueError("expected draft_tokens [B,K] and target [B,K+1,V]")
@@ -146,7 +150,7 @@ def accept_fused(
         draft = uniforms = resample_uniform = None
     tokens = draft_tokens.to(device=dev, dtype=torch.int64).contiguous()
 
-    accepted, mask, out_token, all_acc, posterior = _outputs(B, K, dev)
+    accepted, mask, out_token, all_acc, post = _outputs(B, K, dev, posterior or greedy)
     lib = _lib.load()
     nbytes = lib.d3d_accept_workspace_bytes(B, K, V)
     ws = _lib.workspace(dev, "accept", nbytes)
@@ -155,10 +159,10 @@ def accept_fused(
         _lib.ptr(tokens), _lib.ptr(uniforms), _lib.ptr(resample_uniform),
         float(temperature), B, K, V,
         _lib.ptr(accepted), _lib.ptr(mask), _lib.ptr(out_token), _lib.ptr(all_acc),
-        _lib.ptr(posterior), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
+        _lib.ptr(post), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
     )
     _lib.check(status, "d3d_accept_fused")
-    return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), posterior)
+    return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), post)
 
 
 def accept_fused_sparse(
@@ -172,6 +176,7 @@ def accept_fused_sparse(
     resample_uniform: Optional[torch.Tensor] = None,
     input_kind: str = "probs",
     generator: Optional[torch.Generator] = None,
+    posterior: bool = True,
 ) -> AcceptOutput:
     """Batched fused acceptance against sparse proposals, one launch.
 
@@ -179,7 +184,7 @@ def accept_fused_sparse(
     ``draft_token_ids`` / ``draft_token_probs`` [B, K, S] (S <= 1024), the
     proposal support of single/speculative_sampling.py:79-143.  Support ids
     outside [0, V) carry no mass.  No host synchronisation; statuses in
-    ``out_token`` as for :func:`accept_fused`.
+    ``out_token`` and ``posterior`` as for :func:`accept_fused`.
     """
     if target.ndim != 3 or draft_tokens.ndim != 2:
         raise ValueError("expected draft_tokens [B,K] and target [B,K+1,V]")
@@ -208,17 +213,17 @@ def accept_fused_sparse(
     q_ids = draft_token_ids.to(dtype=torch.int64).contiguous()
     q_probs = draft_token_probs.to(dtype=torch.float32).contiguous()
 
-    accepted, mask, out_token, all_acc, posterior = _outputs(B, K, dev)
+    accepted, mask, out_token, all_acc, post = _outputs(B, K, dev, posterior)
     lib = _lib.load()
     ws = _lib.workspace(dev, "accept", lib.d3d_accept_workspace_bytes(B, K, V))
     status = lib.d3d_accept_fused_sparse(
         _lib.ptr(target), _lib.dtype_code(target), kind, _lib.ptr(tokens), _lib.ptr(q_ids), _lib.ptr(q_probs),
         S, _lib.ptr(uniforms), _lib.ptr(resample_uniform), float(temperature), B, K, V,
         _lib.ptr(accepted), _lib.ptr(mask), _lib.ptr(out_token), _lib.ptr(all_acc),
-        _lib.ptr(posterior), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
+        _lib.ptr(post), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
     )
     _lib.check(status, "d3d_accept_fused_sparse")
-    return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), posterior)
+    return AcceptOutput(accepted, mask.bool(), out_token, all_acc.bool(), post)
 
 
 def _to_result(out: AcceptOutput) -> SpeculativeSampleResult:
@@ -263,7 +268,7 @@ def verify_speculative_block(
     out = accept_fused(
         target_probs, draft_probs, draft_tokens,
         uniforms=uniforms, resample_uniform=resample_uniform,
-        input_kind="probs", generator=generator,
+        input_kind="probs", generator=generator, posterior=False,
     )
     return _to_result(out)
 
@@ -300,6 +305,7 @@ def verify_speculative_block_sparse(
     out = accept_fused_sparse(
         target_probs, draft_tokens, draft_token_ids, draft_token_probs,
         uniforms=uniforms, resample_uniform=resample_uniform, input_kind="probs", generator=generator,
+        posterior=False,
     )
     return _to_result(out)
 

@@ -100,7 +100,8 @@ size_t d3d_accept_workspace_bytes(int B, int K, int64_t V);
  *   out_token    [B] int64  correction token (or bonus token when all K are
  *                accepted); D3D_TOKEN_* sentinels on invalid input
  *   all_accepted [B] uint8
- *   posterior    [B, K+1] int64  argmax of every target row (may be NULL)
+ *   posterior    [B, K+1] int64  argmax of every target row (may be NULL;
+ *                the stochastic modes then skip the argmax reduction)
  */
 int d3d_accept_fused(const void* target, const void* draft, int dtype, int input_kind,
                      const int64_t* draft_tokens, const float* uniforms,

@@ -80,6 +80,25 @@ def test_stochastic_logits_vs_oracle(V, B, K, T, dtype):
     np.testing.assert_array_equal(got["posterior"], t.numpy().argmax(-1))
 
 
+@pytest.mark.parametrize("B,dtype", [(8, torch.float32), (1, torch.bfloat16)])
+def test_stochastic_decision_without_posterior_is_unchanged(B, dtype):
+    """posterior=False skips the argmax reduction of the stochastic modes:
+    the decision (mask, length, token) is the same, bit for bit, and the
+    posterior is not returned; greedy acceptance still returns it."""
+    dev = _dev()
+    inp = workloads.accept_inputs(41 + B, B=B, K=15, V=151936, temperature=1.0)
+    t, d = inp.target.to(dev, dtype), inp.draft.to(dev, dtype)
+    args = (t, d, inp.tokens.to(dev))
+    kw = dict(temperature=1.0, uniforms=inp.uniforms.to(dev), resample_uniform=inp.resample_u.to(dev))
+    full = ss.accept_fused(*args, **kw)
+    bare = ss.accept_fused(*args, posterior=False, **kw)
+    assert bare.posterior is None
+    for key in ("accepted", "accept_mask", "out_token", "all_accepted"):
+        assert torch.equal(getattr(full, key), getattr(bare, key)), key
+    greedy = ss.accept_fused(t, None, inp.tokens.to(dev), temperature=0.0, posterior=False)
+    assert torch.equal(greedy.posterior.cpu(), t.float().cpu().argmax(-1))
+
+
 @pytest.mark.parametrize("V", [64, 4096, 151936])
 def test_stochastic_probs_input_vs_oracle(V):
     inp = workloads.accept_inputs(7, B=6, K=15, V=V)
