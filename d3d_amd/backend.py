@@ -32,6 +32,7 @@ from __future__ import annotations
 
 from typing import Dict, List, Optional, Union
 
+import numpy as np
 import torch
 
 from .draft import topk_tokens
@@ -50,6 +51,16 @@ def _to_host(t: torch.Tensor) -> torch.Tensor:
     buf = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
     buf.copy_(t, non_blocking=True)
     return buf
+
+
+def _host_ids(x):
+    """Token ids or positions [B, Q] as a host array (device tensors pass through)."""
+    if isinstance(x, torch.Tensor):
+        return x if x.is_cuda else x.to(torch.int64).numpy()
+    arr = np.asarray(x, dtype=np.int64)
+    if arr.ndim != 2:
+        raise ValueError(f"expected [B, Q] token ids, got shape {arr.shape}")
+    return arr
 
 
 MASK_ID = 151669
@@ -119,8 +130,9 @@ class Runner:
                 release(self.kv, seq, self.name)
 
     def trim(self, seq: Sequence, length: int) -> None:
-        with torch.cuda.stream(self.stream):
-            trim(self.kv, seq, self.name, length)
+        # Host bookkeeping only: the device table rows are rewritten by the
+        # next block_inputs on this runner's stream.
+        trim(self.kv, seq, self.name, length)
 
     def _tables(self, seqs: List[Sequence]) -> torch.Tensor:
         width = max(len(self.table(s)) for s in seqs)
@@ -150,10 +162,38 @@ class Runner:
                 return None
             return _to_host(self.model.logits(hidden).argmax(-1))
 
-    def _inputs(self, seqs: List[Sequence], Q: int):
+    def _prepare(self, seqs: List[Sequence], Q: int, kind: str, vis: Optional[torch.Tensor], k: int) -> BlockStep:
+        """Reserve the block's pages and write its page tables, slots,
+        context lengths and positions straight into the step's static
+        buffers (on the runner's stream); returns the step.  A step that
+        ``prepare`` already filled for the same requests, prefixes and page
+        lists is returned as it is."""
         for s in seqs:
             self.reserve(s, s.prefix + Q)
-        return block_inputs(self.kv, seqs, self.name, [s.prefix for s in seqs], Q, self.device, self.width)
+        width = self.width if self.width is not None else max(len(self.table(s)) for s in seqs)
+        step = self._step(kind, len(seqs), Q, width, vis, k)
+        key = tuple((s.seq_id, s.prefix, tuple(self.table(s))) for s in seqs)
+        if step.prepared == key:
+            step.prepared = None
+            return step
+        step.prepared = None
+        block_inputs(self.kv, seqs, self.name, [s.prefix for s in seqs], Q, self.device, width, out=step.inputs())
+        return step
+
+    def prepare(self, seqs: List[Sequence], Q: int, *, mask_builder=None, topk: int = 0) -> None:
+        """Fill the page tables, slots and context lengths of the next block
+        forward over ``seqs`` (Q tokens at their prefixes) ahead of it, on
+        the runner's stream, so that the forward itself only copies its
+        token ids and replays.  The next ``forward`` / ``verify`` with the
+        same requests, prefixes, page lists and block shape uses them;
+        anything else prepares again."""
+        with torch.cuda.stream(self.stream):
+            if self.draft:
+                vis = self._visibility(seqs, Q, mask_builder)
+                step = self._prepare(seqs, Q, "forward", vis, topk)
+            else:
+                step = self._prepare(seqs, Q, "verify", None, 0)
+            step.prepared = tuple((s.seq_id, s.prefix, tuple(self.table(s))) for s in seqs)
 
     def _step(self, kind: str, B: int, Q: int, width: int, vis: Optional[torch.Tensor], k: int):
         key = (kind, B, Q, width, k, None if vis is None else (tuple(vis.shape), vis.numpy().tobytes()))
@@ -180,15 +220,11 @@ class Runner:
         With ``host`` the results are pinned host tensors whose copies are
         queued on the runner's stream (valid once it has drained)."""
         with torch.cuda.stream(self.stream):
-            ids = torch.as_tensor(tokens, dtype=torch.long).to(self.device, non_blocking=True)
+            ids = _host_ids(tokens)
             B, Q = ids.shape
-            tables, slots, lens, logical, _ = self._inputs(seqs, Q)
-            vis = None
-            if self.draft:
-                vis = self._visibility(seqs, Q, mask_builder)
-            pos = logical if positions is None else torch.as_tensor(positions).to(self.device, non_blocking=True)
-            step = self._step("forward", B, Q, tables.shape[1], vis, topk)
-            top, greedy = step(ids, pos, tables, slots, lens)
+            vis = self._visibility(seqs, Q, mask_builder) if self.draft else None
+            step = self._prepare(seqs, Q, "forward", vis, topk)
+            top, greedy = step.run(ids, None if positions is None else _host_ids(positions))
             copy = _to_host if host else torch.clone
             if topk:
                 return copy(top[..., :topk].contiguous()), copy(greedy)
@@ -204,11 +240,9 @@ class Runner:
         if self.draft:
             raise RuntimeError("verify runs on the target runner")
         with torch.cuda.stream(self.stream):
-            ids = torch.as_tensor(tokens, dtype=torch.long).to(self.device, non_blocking=True)
+            ids = _host_ids(tokens)
             B, Q = ids.shape
-            tables, slots, lens, logical, _ = self._inputs(seqs, Q)
-            accepted, out_token = self._step("verify", B, Q, tables.shape[1], None, 0)(ids, logical, tables,
-                                                                                       slots, lens)
+            accepted, out_token = self._prepare(seqs, Q, "verify", None, 0).run(ids)
             return _to_host(torch.stack([accepted.long() + 1, out_token]))
 
     def _visibility(self, seqs: List[Sequence], Q: int, mask_builder) -> torch.Tensor:

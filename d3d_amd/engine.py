@@ -211,12 +211,35 @@ class Engine:
 
     def _recover(self, seqs: List[Sequence]) -> None:
         """serving/engine.py:54-62: s.current = [anchor, draft greedy ...], s.top = top-(A+1)."""
-        for group, top, greedy in self._recover_submit(seqs, self.A + 1):
-            self.draft.stream.synchronize()
+        out = self._recover_submit(seqs, self.A + 1)
+        self.draft.stream.synchronize()
+        self._apply_recovered(out)
+
+    @staticmethod
+    def _apply_recovered(out) -> None:
+        """Adopt finished recovery forwards (their host copies complete)."""
+        for group, top, greedy in out:
             for s, blk, t in zip(group, greedy.tolist(), top.tolist()):
                 blk[0] = s.anchor
                 s.current, s.top = blk, t
                 s.recoveries += 1
+
+    def _prepare_next(self, seqs: List[Sequence]) -> None:
+        """Page tables, slots and context lengths of the next step's verify
+        and packed prediction, filled while this step's recovery runs (the
+        prefixes are final once the verify result is applied).  The packed
+        layout (accepted count per branch) does not depend on the tokens.
+        Skipped where the next prediction seeds fast backups (other
+        layouts); a layout that does not match is prepared again."""
+        K, A = self.K, self.A
+        self.target.prepare(seqs, K)
+        if self.backup == "fast" and any(s.needs_fast_seed for s in seqs):
+            return
+        layout = [(n, None) for n in range(1, K) for _ in range(A)] + [(K, None)]
+        Q = K + len(layout) * K
+        for off in range(0, len(seqs), self.micro):
+            group = seqs[off:off + self.micro]
+            self.draft.prepare(group, Q, mask_builder=self._mask([layout] * len(group)), topk=A + 1)
 
     def _fast_backup(self, seqs: List[Sequence]) -> None:
         """serving/engine.py:64-71: a random block after the anchor (greedy
@@ -273,8 +296,13 @@ class Engine:
             pending.append((group, specs, top, greedy))
         return pending
 
-    def _predict_collect(self, pending) -> Dict[int, Dict]:
-        self.draft.stream.synchronize()
+    def _predict_collect(self, pending, done: Optional[torch.cuda.Event] = None) -> Dict[int, Dict]:
+        """The packed predictions as host lists, once the draft stream has
+        drained (or once ``done``, an event recorded after them, has)."""
+        if done is None:
+            self.draft.stream.synchronize()
+        else:
+            done.synchronize()
         K = self.K
         results: Dict[int, Dict] = {}
         for group, specs, top, greedy in pending:
@@ -400,11 +428,13 @@ class Engine:
             ev["ps"].record(self.draft.stream)
             pending = self._side("draft", self._predict_submit, running)
             ev["pe"].record(self.draft.stream)
-            predictions = self._side("draft", self._predict_collect, pending)
+            # The verify result decides the step; the predictions are read
+            # once the recovery forwards are queued behind them.
             self._side("target", self.target.stream.synchronize)
             accepted = list(zip(*res.tolist()))
+            predicted = {s.seq_id: set(specs[b]) for group, specs, _, _ in pending for b, s in enumerate(group)}
             steps += 1
-            remaining, recover = [], []
+            remaining, recover, hits = [], [], []
             for s, block, (n, anchor) in zip(running, blocks, accepted):
                 n, anchor = int(n), int(anchor)
                 emitted = block[:n][: max_new_tokens - len(s.generated)]
@@ -426,13 +456,10 @@ class Engine:
                     self._finish(s, outputs)
                     continue
                 key = (n, None if n == K else anchor)
-                selected = predictions[s.seq_id].get(key)
-                if selected is None:
-                    recover.append(s)
+                if key in predicted[s.seq_id]:
+                    hits.append((s, key, anchor))
                 else:
-                    s.current, s.top = list(selected[0]), selected[1]
-                    s.current[0] = anchor
-                    s.hits += 1
+                    recover.append(s)
                 self.target.trim(s, s.prefix)
                 self.draft.trim(s, s.prefix)
                 remaining.append(s)
@@ -440,12 +467,24 @@ class Engine:
             miss_rounds += bool(recover)
             miss_requests += len(recover)
             ev["rs"].record(self.draft.stream)
+            recovered = []
             if self.backup in ("fast", "fast_legacy"):
                 self._fast_backup(recover)
-            else:
-                self._side("draft", self._recover, recover)
+            elif recover:
+                recovered = self._side("draft", self._recover_submit, recover, self.A + 1)
             ev["re"].record(self.draft.stream)
-            ev["re"].synchronize()
+            if running and (exhausted or len(running) >= concurrency):
+                self._side("draft", self._prepare_next, running)
+            # The predictions finished before the verify did: read them
+            # while the recovery forwards run.
+            predictions = self._side("draft", self._predict_collect, pending, ev["pe"])
+            for s, key, anchor in hits:
+                selected = predictions[s.seq_id][key]
+                s.current, s.top = list(selected[0]), selected[1]
+                s.current[0] = anchor
+                s.hits += 1
+            self._side("draft", self.draft.stream.synchronize)
+            self._apply_recovered(recovered)
             decode_s += time.perf_counter() - t_step
             vs, ve = origin.elapsed_time(ev["vs"]), origin.elapsed_time(ev["ve"])
             ps_, pe = origin.elapsed_time(ev["ps"]), origin.elapsed_time(ev["pe"])

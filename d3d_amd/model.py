@@ -31,6 +31,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -114,19 +115,41 @@ class DevicePageTables:
             seq.synced[name] = [0, 0]
         return row
 
-    def sync(self, seq: "Sequence", name: str) -> None:
-        """Copy the page ids appended since the last sync; mark the ids a trim removed -1."""
+    def updates(self, seq: "Sequence", name: str) -> tuple:
+        """The pool entries to rewrite for seq's table ``name``: (flat
+        indices, values) of the page ids appended since the last sync and
+        of the -1 marks over the ids a trim removed.  The caller applies
+        them (``apply``) before the table is next read on the device."""
         row = self.row(seq, name)
         pages = seq.pages.get(name, [])
         state = seq.synced[name]  # [entries equal to the host list, entries written]
         valid, written = state
-        if len(pages) > valid:
-            new = torch.empty(len(pages) - valid, dtype=torch.int32, pin_memory=True)
-            new.copy_(torch.tensor(pages[valid:], dtype=torch.int32))
-            self.pool[row, valid:len(pages)].copy_(new, non_blocking=True)
-        if written > len(pages):
-            self.pool[row, len(pages):written].fill_(-1)
-        state[0] = state[1] = len(pages)
+        n = len(pages)
+        state[0] = state[1] = n
+        if n > valid:
+            cols = np.arange(valid, max(n, written), dtype=np.int64)
+            vals = np.full(len(cols), -1, dtype=np.int64)
+            vals[: n - valid] = pages[valid:]
+        elif written > n:
+            cols = np.arange(n, written, dtype=np.int64)
+            vals = np.full(len(cols), -1, dtype=np.int64)
+        else:
+            return None
+        return row * self.width + cols, vals
+
+    def apply(self, flat: torch.Tensor, vals: torch.Tensor) -> None:
+        """pool.flat[flat[i]] = vals[i] on the current stream (device int32 tensors)."""
+        if self.pool.numel() >= 2 ** 31:
+            raise ValueError("page-table pool too large for int32 entry indices")
+        self.pool.view(-1).index_put_((flat.long(),), vals)
+
+    def sync(self, seq: "Sequence", name: str) -> None:
+        """Copy the page ids appended since the last sync; mark the ids a trim removed -1."""
+        upd = self.updates(seq, name)
+        if upd is not None:
+            h = torch.from_numpy(np.stack(upd).astype(np.int32)).pin_memory()
+            d = h.to(self.device, non_blocking=True)
+            self.apply(d[0], d[1])
 
     def drop(self, seq: "Sequence", name: str) -> None:
         row = seq.rows.pop(name, None)
@@ -263,7 +286,7 @@ def release(kv: PagedKV, seq: Sequence, name: str) -> None:
 
 
 def block_inputs(kv: PagedKV, seqs: List[Sequence], name: str, starts: List[int], Q: int, device,
-                 width: Optional[int] = None):
+                 width: Optional[int] = None, out: Optional[tuple] = None):
     """Page tables, slots and context lengths for a block of Q tokens at starts[b].
 
     ``width`` fixes the page-table width (and so the attention's context
@@ -271,6 +294,9 @@ def block_inputs(kv: PagedKV, seqs: List[Sequence], name: str, starts: List[int]
     tables come from the device mirror: per step only the request rows and
     starts cross to the device, and one kernel gathers the tables and
     computes the slot mapping (serving/backend.py:73-76, :123-124).
+    ``out`` = (tables [B, width] int32, slots [B*Q] int64, logical [B, Q]
+    int64, lens [B] int32) receives the results in place (a block step's
+    static buffers) instead of new tensors.
     """
     width = max(len(s.pages[name]) for s in seqs) if width is None else width
     if any(len(s.pages[name]) > width for s in seqs):
@@ -279,16 +305,35 @@ def block_inputs(kv: PagedKV, seqs: List[Sequence], name: str, starts: List[int]
     dev = torch.device(device)
     T = kv.tables
     B = len(seqs)
-    host = torch.empty(2, B, dtype=torch.int32, pin_memory=True)
-    for b, s in enumerate(seqs):
-        T.sync(s, name)
-        host[0, b] = T.row(s, name)
-        host[1, b] = int(starts[b])
-    ri = host.to(dev, non_blocking=True)
-    tables = torch.empty(B, width, dtype=torch.int32, device=dev)
-    slots = torch.empty(B * Q, dtype=torch.int64, device=dev)
-    logical = torch.empty(B, Q, dtype=torch.int64, device=dev)
-    lens = torch.empty(B, dtype=torch.int32, device=dev)
+    # One pinned buffer, one copy: the request rows and starts, then the
+    # page-table entries to rewrite (appended pages, -1 over trimmed ones)
+    # of every request.
+    rows = [T.row(s, name) for s in seqs]
+    upds = [u for u in (T.updates(s, name) for s in seqs) if u is not None]
+    n = sum(len(u[0]) for u in upds)
+    host = torch.empty(2 * B + 2 * n, dtype=torch.int32, pin_memory=True)
+    hn = host.numpy()
+    hn[:B] = rows
+    hn[B:2 * B] = [int(x) for x in starts]
+    if n:
+        hn[2 * B:2 * B + n] = np.concatenate([u[0] for u in upds])
+        hn[2 * B + n:] = np.concatenate([u[1] for u in upds])
+    dh = host.to(dev, non_blocking=True)
+    if n:
+        T.apply(dh[2 * B:2 * B + n], dh[2 * B + n:])
+    ri = dh[:2 * B].view(2, B)
+    if out is None:
+        tables = torch.empty(B, width, dtype=torch.int32, device=dev)
+        slots = torch.empty(B * Q, dtype=torch.int64, device=dev)
+        logical = torch.empty(B, Q, dtype=torch.int64, device=dev)
+        lens = torch.empty(B, dtype=torch.int32, device=dev)
+    else:
+        tables, slots, logical, lens = out
+        if (tuple(tables.shape) != (B, width) or tables.dtype != torch.int32 or slots.numel() != B * Q
+                or slots.dtype != torch.int64 or tuple(logical.shape) != (B, Q) or logical.dtype != torch.int64
+                or tuple(lens.shape) != (B,) or lens.dtype != torch.int32
+                or not all(t.is_contiguous() and t.device == dev for t in out)):
+            raise ValueError("block_inputs out buffers do not match the block")
     st = _lib.load().d3d_block_inputs(T.pool.data_ptr(), T.pool.shape[0], T.width, ri[0].data_ptr(),
                                       ri[1].data_ptr(), B, int(Q), int(width), kv.page_size, tables.data_ptr(),
                                       slots.data_ptr(), logical.data_ptr(), lens.data_ptr(), _lib.stream_ptr(dev))
@@ -334,6 +379,7 @@ class BlockStep:
         self.graph = None
         self.out = None
         self.workspaces: list = []
+        self.prepared = None  # the requests whose block inputs the static buffers hold
         from .streams import register_graph_owner
         register_graph_owner(self)
 
@@ -365,9 +411,30 @@ class BlockStep:
 
     def _call(self, ids, pos, tables, slots, lens):
         self._load(ids, pos, tables, slots, lens)
+        return self._replay()
+
+    def inputs(self) -> tuple:
+        """The static (tables, slots, positions, lens) buffers, in
+        ``block_inputs``'s ``out`` order."""
+        return self.tables, self.slots, self.pos, self.lens
+
+    def run(self, ids, pos=None):
+        """Replay on token ids (and positions) given as host arrays, after
+        ``block_inputs(..., out=self.inputs())`` has filled the page tables,
+        slots, context lengths and default positions on the stream.  The
+        host arrays cross in one pinned copy each."""
+        with torch.inference_mode():
+            _stage(self.ids, ids)
+            if pos is not None:
+                _stage(self.pos, pos)
+            return self._replay()
+
+    def _replay(self):
         if not self.use_graph:
             return self._body()
         if self.graph is None:
+            bufs = (self.ids, self.pos, self.tables, self.slots, self.lens)
+            saved = [t.clone() for t in bufs]
             cur = torch.cuda.current_stream(self.model.device)
             side = _warmup_stream(self.model.device)
             side.wait_stream(cur)
@@ -380,9 +447,24 @@ class BlockStep:
                 self.out = self._body()
             self.graph = g
             # The warm-up may have updated the static inputs in place.
-            self._load(ids, pos, tables, slots, lens)
+            for t, v in zip(bufs, saved):
+                t.copy_(v)
         self.graph.replay()
         return self.out
+
+
+def _stage(dst: torch.Tensor, src) -> None:
+    """dst (device, int64) <- src (host list, numpy array or tensor) through
+    a pinned buffer, queued on the current stream."""
+    if isinstance(src, torch.Tensor) and src.is_cuda:
+        dst.copy_(src.reshape(dst.shape), non_blocking=True)
+        return
+    arr = src.numpy() if isinstance(src, torch.Tensor) else np.asarray(src)
+    if arr.size != dst.numel():
+        raise ValueError(f"expected {tuple(dst.shape)} values, got {arr.shape}")
+    h = torch.empty(dst.shape, dtype=torch.int64, pin_memory=True)
+    h.numpy()[...] = arr.reshape(dst.shape)
+    dst.copy_(h, non_blocking=True)
 
 
 def prefill(model: Qwen3PagedModel, kv: PagedKV, seqs: List[Sequence], name: str, block: int = 16) -> torch.Tensor:

@@ -4,6 +4,8 @@ from __future__ import annotations
 
 import random
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -102,3 +104,45 @@ def test_split_product_rejects_a_leading_dimension_other_than_splits():
     for parts, splits in ((torch.zeros(2, 4, 8), 3), (torch.zeros(4, 8), 1), (torch.zeros(0, 4, 8), 0)):
         with pytest.raises(ValueError, match="split partials must be"):
             SplitProduct(parts, splits)
+
+
+def test_page_table_updates_keep_the_mirror_equal_to_the_host_lists():
+    """DevicePageTables.updates/apply (the entries block_inputs rewrites in
+    one copy) on a CPU pool: after every reserve / trim / re-reserve of the
+    engine's step pattern (a 272-token packed block reserved, the tail
+    trimmed, reserved again) each row holds the host page list, then -1."""
+    from d3d_amd.model import DevicePageTables, PagePool, Sequence, reserve, trim
+
+    class _KV:  # the two members reserve/trim use
+        page_size = 16
+        pool = PagePool(256)
+
+    kv = _KV()
+    kv.tables = DevicePageTables(256, "cpu", rows=2)  # grows past two rows
+    rng = random.Random(5)
+    seqs = [Sequence(i, [0] * (20 + 9 * i)) for i in range(5)]
+
+    def check():
+        upds = [u for u in (kv.tables.updates(s, "d") for s in seqs) if u is not None]
+        if upds:
+            flat = torch.from_numpy(np.concatenate([u[0] for u in upds]).astype(np.int32))
+            vals = torch.from_numpy(np.concatenate([u[1] for u in upds]).astype(np.int32))
+            kv.tables.apply(flat, vals)
+        for s in seqs:
+            row = kv.tables.pool[s.rows["d"]].tolist()
+            n = len(s.pages["d"])
+            assert row[:n] == s.pages["d"] and all(v == -1 for v in row[n:])
+        assert all(kv.tables.updates(s, "d") is None for s in seqs)  # nothing left to write
+
+    for step in range(12):
+        for s in seqs:
+            reserve(kv, s, "d", s.prefix + 272)
+        check()
+        for s in seqs:
+            s.prefix += rng.randint(1, 16)
+            trim(kv, s, "d", s.prefix)
+        if step % 3 == 2:
+            check()  # trims alone: -1 over the released entries
+        for s in seqs:
+            reserve(kv, s, "d", s.prefix + 16)
+        check()
