@@ -17,7 +17,7 @@ iterations over their wall time (admission and prefill excluded).
 
 ``rooflines`` lists the kernels each configuration names, each timed with
 HIP events over repeated calls replayed from one HIP graph (the form the
-engine runs them in); every call reads the next of several input sets
+engine runs them in; the median of five timed blocks of calls); every call reads the next of several input sets
 totalling over 640 MB, so its inputs come from HBM rather than the 256 MB
 memory-side cache; ``frac`` = algorithmic bytes / call duration / 8 TB/s:
 
@@ -288,11 +288,13 @@ def gemm_rows64_bench(dev, calls: int):
     return out
 
 
-def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40) -> float:
-    """Average milliseconds per call with the calls replayed from a HIP graph
-    (the form the engine runs them in) of ``per_graph`` consecutive calls
-    cycling through the input sets: events on the replay stream, bracketed
-    by synchronisations."""
+def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40, blocks: int = 5) -> float:
+    """Milliseconds per call with the calls replayed from a HIP graph (the
+    form the engine runs them in) of ``per_graph`` consecutive calls cycling
+    through the input sets: events on the replay stream, bracketed by
+    synchronisations.  ``blocks`` timed blocks of ``calls`` calls each; the
+    median block is returned (the first block of a process can run several
+    microseconds per call slower while the GPU settles)."""
     s = torch.cuda.Stream(dev)
     for c in r.calls:
         c.bind_stream(s.cuda_stream)
@@ -308,14 +310,17 @@ def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40)
             g.replay()
         torch.cuda.synchronize(dev)
         reps = max(1, -(-calls // per_graph))
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(s)
-        for _ in range(reps):
-            g.replay()
-        end.record(s)
-        torch.cuda.synchronize(dev)
+        times = []
+        for _ in range(blocks):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(s)
+            for _ in range(reps):
+                g.replay()
+            end.record(s)
+            torch.cuda.synchronize(dev)
+            times.append(start.elapsed_time(end) / (reps * per_graph))
     del g
-    return start.elapsed_time(end) / (reps * per_graph)
+    return statistics.median(times)
 
 
 def time_calls(fn, steps: int, warmup: int, dev) -> float:
