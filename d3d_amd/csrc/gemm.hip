@@ -6,13 +6,24 @@
 // weight once and each activation once per 64 output columns), so the
 // kernel is built to stream W:
 //
-// * Workgroup (column tile of 64, K split s): four waves; each k step moves
-//   a 64 x 128 tile of W and the 64 x 128 tile of X straight from global
-//   memory into LDS (global_load_lds, 16 bytes per lane: every wave
-//   instruction reads four full 256-byte row segments), two stages deep, so
-//   the loads in flight cost no registers.  Within a row the 16-byte chunk
-//   q is stored at slot q ^ (row & 7): the MFMA operand reads of 16
-//   consecutive rows then spread over the LDS banks.
+// * Workgroup (column tile of 64, K split s), four waves; each k step moves
+//   a 64 x 128 tile of W and the 64 x 128 tile of X.  Every wave
+//   instruction reads four full 256-byte row segments (16 bytes per lane),
+//   the order that streams the weights fastest of those measured.  Within
+//   a row the 16-byte chunk q is stored at slot q ^ (row & 7) of LDS, so
+//   the MFMA operand reads of 16 consecutive rows spread over the banks.
+// * Register-staged pipeline (gemm_rows64_kernel): the loads of the next
+//   two k steps are in flight in registers while a step is stored to one of
+//   two LDS buffers and multiplied from it, one barrier per step.  The k
+//   loop is unrolled for the step counts the models use (STEPS), so the
+//   compiler's wait before each store counts exactly the loads issued after
+//   it.  Measured against the earlier form (direct global -> LDS loads, two
+//   stages, two barriers per step; kept as gemm_rows64_dma_kernel for other
+//   step counts), graph-replayed on HBM-resident weights: target o 14.7 ->
+//   9.9 us, target down 29.8 -> 23.5, draft qkv 9.2 -> 7.1, draft o 6.7 ->
+//   6.0, draft down 12.4 -> 8.9; the same kernel without loads of X or
+//   without the MFMAs was only 10-15 % faster, so the direct-to-LDS loads
+//   with one stage ahead were the bound.
 // * Wave w multiplies the 64 rows of X by columns 16w .. 16w + 15 of the
 //   tile with v_mfma_f32_16x16x32_bf16, both operands read from LDS.
 // * Small N leaves too few column tiles to fill 256 CUs, so K is split over
@@ -50,7 +61,48 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ __launch_bounds__(NT) void gemm_rows64_kernel(const uint16_t* __restrict__ x,
+// One k step from an LDS stage (W tile, then X tile): wave wv multiplies the
+// 64 rows of X by columns 16 wv .. 16 wv + 15 of the tile.
+__device__ __forceinline__ void mma_step(const char* cur, f32x4 (&acc)[4], int wv, int c16, int g4) {
+    const int rB = 16 * wv + c16;
+#pragma unroll
+    for (int ks = 0; ks < TK / 32; ++ks) {
+        const int q = 4 * ks + g4;
+        const u32x4 bw = *reinterpret_cast<const u32x4*>(cur + rB * ROWB + 16 * (q ^ (rB & 7)));
+        u32x4 ax[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int m = 16 * t + c16;
+            ax[t] = *reinterpret_cast<const u32x4*>(cur + TILEB + m * ROWB + 16 * (q ^ (m & 7)));
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ax[t]),
+                                                             __builtin_bit_cast(bf16x8, bw), acc[t], 0, 0, 0);
+    }
+}
+
+// Lane (c16, g4) holds rows 16t + 4 g4 + r of column n: bf16 into Y (one
+// split) or the fp32 partial of split blockIdx.y.
+__device__ __forceinline__ void store_tile(const f32x4 (&acc)[4], uint16_t* y, float* parts, int M, int N, int n,
+                                           int g4) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * t + 4 * g4 + r;
+            if (m < M) {
+                if (gridDim.y == 1)
+                    y[(size_t)m * N + n] = f32_to_bf16_bits(acc[t][r]);
+                else
+                    parts[((size_t)blockIdx.y * M + m) * N + n] = acc[t][r];
+            }
+        }
+}
+
+// Direct global -> LDS form (global_load_lds, two stages): the kernel for
+// step counts gemm_rows64_kernel is not unrolled for.
+__global__ __launch_bounds__(NT) void gemm_rows64_dma_kernel(const uint16_t* __restrict__ x,
                                                          const uint16_t* __restrict__ w,
                                                          uint16_t* __restrict__ y, float* __restrict__ parts,
                                                          int M, int N, int K, int KR) {
@@ -86,7 +138,6 @@ __global__ __launch_bounds__(NT) void gemm_rows64_kernel(const uint16_t* __restr
         __builtin_amdgcn_global_load_lds(wsrc[j], smem + lofs[j], 16, 0, 0);
         __builtin_amdgcn_global_load_lds(xsrc[j], smem + TILEB + lofs[j], 16, 0, 0);
     }
-    const int rB = 16 * wv + c16;
     for (int step = 0; step < steps; ++step) {
         if (step + 1 < steps) {
             char* nxt = smem + ((step + 1) % ST) * STAGEB;
@@ -101,38 +152,70 @@ __global__ __launch_bounds__(NT) void gemm_rows64_kernel(const uint16_t* __restr
             wait_vmcnt<0>();
         }
         __syncthreads();
-        const char* cur = smem + (step % ST) * STAGEB;
-#pragma unroll
-        for (int ks = 0; ks < TK / 32; ++ks) {
-            const int q = 4 * ks + g4;
-            const u32x4 bw = *reinterpret_cast<const u32x4*>(cur + rB * ROWB + 16 * (q ^ (rB & 7)));
-            u32x4 ax[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int m = 16 * t + c16;
-                ax[t] = *reinterpret_cast<const u32x4*>(cur + TILEB + m * ROWB + 16 * (q ^ (m & 7)));
-            }
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ax[t]),
-                                                                 __builtin_bit_cast(bf16x8, bw), acc[t], 0, 0, 0);
-        }
+        mma_step(smem + (step % ST) * STAGEB, acc, wv, c16, g4);
         __syncthreads();
     }
-    // Lane (c16, g4) holds rows 16t + 4 g4 + r of column 16 wv + c16.
-    const int n = n0 + 16 * wv + c16;
+    store_tile(acc, y, parts, M, N, n0 + 16 * wv + c16, g4);
+}
+
+// Register-staged form of the kernel above (same tiles, LDS layout and
+// results): stage st of a lane is rw / rx[st % 2] until it is stored to
+// LDS buffer st % 2; the loads of stage st + 2 then reuse those registers.
+template <int STEPS>
+__global__ __launch_bounds__(NT, 2) void gemm_rows64_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ w,
+                                                            uint16_t* __restrict__ y, float* __restrict__ parts,
+                                                            int M, int N, int K, int KR) {
+    constexpr int P = 2;  // k steps in flight in registers
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+    const int c16 = lane & 15, g4 = lane >> 4;
+    const int n0 = blockIdx.x * TN;
+    const int kb = blockIdx.y * KR;
+    // This lane's source rows and LDS slots: wave wv loads rows
+    // (wv * LPW + j) * RPI + lane / CPR of both tiles, global chunk
+    // (lane % CPR) ^ (row & 7) into LDS chunk lane % CPR.
+    const int lr = lane / CPR, lc = lane % CPR;
+    const uint16_t* wsrc[LPW];
+    const uint16_t* xsrc[LPW];
+    int lofs[LPW];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int j = 0; j < LPW; ++j) {
+        const int r = (wv * LPW + j) * RPI + lr;
+        const int q = lc ^ (r & 7);
+        wsrc[j] = w + (size_t)(n0 + r) * K + kb + 8 * q;
+        xsrc[j] = x + (size_t)min(r, M - 1) * K + kb + 8 * q;
+        lofs[j] = r * ROWB + lc * 16;
+    }
+    u32x4 rw[P][LPW], rx[P][LPW];
+    auto load = [&](int st, int sl) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 16 * t + 4 * g4 + r;
-            if (m < M) {
-                if (gridDim.y == 1)
-                    y[(size_t)m * N + n] = f32_to_bf16_bits(acc[t][r]);
-                else
-                    parts[((size_t)blockIdx.y * M + m) * N + n] = acc[t][r];
-            }
+        for (int j = 0; j < LPW; ++j) {
+            rw[sl][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wsrc[j] + st * TK));
+            rx[sl][j] = *reinterpret_cast<const u32x4*>(xsrc[j] + st * TK);
         }
+    };
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+        if (p < STEPS) load(p, p);
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+        // Buffer st % 2 was last read in step st - 2, which every wave
+        // finished before the barrier of step st - 1.
+        char* buf = smem + (st & 1) * STAGEB;
+#pragma unroll
+        for (int j = 0; j < LPW; ++j) {
+            *reinterpret_cast<u32x4*>(buf + lofs[j]) = rw[st % P][j];
+            *reinterpret_cast<u32x4*>(buf + TILEB + lofs[j]) = rx[st % P][j];
+        }
+        if (st + P < STEPS) load(st + P, st % P);
+        __syncthreads();
+        mma_step(buf, acc, wv, c16, g4);
+    }
+    store_tile(acc, y, parts, M, N, n0 + 16 * wv + c16, g4);
 }
 
 }  // namespace gemm
@@ -163,9 +246,22 @@ extern "C" int d3d_gemm_rows64(const void* x, const void* w, void* y, float* par
     if (splits < 1 || splits > gemm::kMaxSplits || K % (gemm::TK * splits)) return D3D_E_SHAPE;
     if (!x || !w || (splits == 1 ? !y : !parts)) return D3D_E_NULL;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16) return D3D_E_UNSUPPORTED;
-    hipLaunchKernelGGL(gemm::gemm_rows64_kernel, dim3(N / gemm::TN, splits), dim3(gemm::NT), gemm::ST * gemm::STAGEB,
-                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x),
-                       static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), parts, M, N, K, K / splits);
+    const dim3 grid(N / gemm::TN, splits), block(gemm::NT);
+    const size_t lds = gemm::ST * gemm::STAGEB;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    const uint16_t* wp = static_cast<const uint16_t*>(w);
+    uint16_t* yp = static_cast<uint16_t*>(y);
+    const int KR = K / splits;
+    switch (KR / gemm::TK) {
+#define D3D_ROWS64_STEPS(n) \
+    case n: hipLaunchKernelGGL(gemm::gemm_rows64_kernel<n>, grid, block, lds, s, xp, wp, yp, parts, M, N, K, KR); break;
+        D3D_ROWS64_STEPS(1) D3D_ROWS64_STEPS(2) D3D_ROWS64_STEPS(3) D3D_ROWS64_STEPS(4) D3D_ROWS64_STEPS(6)
+        D3D_ROWS64_STEPS(8) D3D_ROWS64_STEPS(12) D3D_ROWS64_STEPS(16) D3D_ROWS64_STEPS(24) D3D_ROWS64_STEPS(32)
+#undef D3D_ROWS64_STEPS
+        default:
+            hipLaunchKernelGGL(gemm::gemm_rows64_dma_kernel, grid, block, lds, s, xp, wp, yp, parts, M, N, K, KR);
+    }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }

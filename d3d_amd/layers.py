@@ -61,25 +61,29 @@ def rows64_splits(N: int, K: int) -> int:
     """The split count project() runs d3d_gemm_rows64 with for a 64-row
     block times weight [N, K], or 0 where it uses hipBLASLt instead.
 
-    Only grids of exactly one or two workgroups per CU (256 CUs, N / 64
-    column tiles times the splits) beat hipBLASLt: fewer leave CUs idle (the
-    6144 x 4096 target qkv at 192), a round and a half leaves half of them
-    idle at the end (the 24576 x 4096 target gate-up at 384).
+    The kernel holds two workgroups per CU (256 CUs); its grid is N / 64
+    column tiles times the splits.  Grids of 128 to 256 workgroups and of
+    exactly 512 beat hipBLASLt on every 64-row projection of both models
+    (graph-replayed, HBM-resident weights): the 6144 x 4096 target qkv at
+    192 workgroups 16.6 against 18.2 us, the 12288 x 2048 draft gate-up at
+    192 14.8 against 17.2 us.  A round and a half (the 24576 x 4096 target
+    gate-up at 384: 48.0 against 46.9 us) and smaller grids stay with
+    hipBLASLt.
     """
     if N % 64 or K % 128:
         return 0
     splits = _lib.load().d3d_gemm_rows64_splits(N, K)
-    return splits if (N // 64) * splits in (256, 512) else 0
+    grid = (N // 64) * splits
+    return splits if 128 <= grid <= 256 or grid == 512 else 0
 
 
 def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
     """F.linear(x, weight) for bf16 x [M, K] and weight [N, K].
 
     Contiguous, 16-byte aligned blocks of at most 64 rows with N % 64 == 0
-    and K % 128 == 0 run d3d_gemm_rows64 when its grid (N / 64 column tiles
-    times the split count) is one or two workgroups per CU; when it splits K
-    the result is a SplitProduct for add_rmsnorm or qk_rope_append to
-    consume.  Other shapes use F.linear (hipBLASLt).
+    and K % 128 == 0 run d3d_gemm_rows64 where rows64_splits says so; when
+    it splits K the result is a SplitProduct for add_rmsnorm or
+    qk_rope_append to consume.  Other shapes use F.linear (hipBLASLt).
     """
     M, K = x.shape
     N = weight.shape[0]

@@ -179,8 +179,9 @@ class Qwen3PagedModel(torch.nn.Module):
     def __init__(self, shape: ModelShape, device, *, draft: bool, seed: int = 0, init_std: float = 0.02):
         super().__init__()
         self.shape, self.draft, self.device = shape, draft, torch.device(device)
-        # Blocks of at most 64 tokens run the QKV, O and down projections on
-        # the weight-streaming HIP GEMM (layers.project) unless this is off.
+        # Blocks of at most 64 tokens run their projections through
+        # layers.project (the weight-streaming HIP GEMM where it is faster
+        # than hipBLASLt) unless this is off.
         self.rows64_gemm = True
         g = torch.Generator(device=self.device).manual_seed(seed)
         h, d, Hq, Hkv = shape.hidden, shape.head_dim, shape.heads, shape.kv_heads
@@ -216,10 +217,11 @@ class Qwen3PagedModel(torch.nn.Module):
         add + RMSNorm, QKV GEMM, fused q/k norm + RoPE + KV append, paged
         attention, O GEMM, fused add + RMSNorm, gate-up GEMM, fused SiLU-mul,
         down GEMM (the decoder layer of serving/vendor/ssd/models/qwen3.py).
-        Blocks of at most 64 tokens run the QKV, O and down GEMMs on the
-        weight-streaming HIP GEMM (layers.project, when ``rows64_gemm``), whose
-        K-split partials the next fused kernel sums; the gate-up GEMM and
-        larger blocks use F.linear.
+        Blocks of at most 64 tokens run the projections on the
+        weight-streaming HIP GEMM where layers.project picks it (when
+        ``rows64_gemm``: the QKV, O and down GEMMs, whose K-split partials the
+        next fused kernel sums, and the draft's gate-up); the target's gate-up
+        and larger blocks use F.linear.
         """
         B, Q = ids.shape
         s = self.shape
@@ -242,7 +244,10 @@ class Qwen3PagedModel(torch.nn.Module):
                                           q_vis, max_seqlen_k=max_context)
             x = proj(o.reshape(B * Q, Hq * d), L["o"])
             ly.add_rmsnorm(x, residual, L["ln2"], s.eps, out=hs)
-            x = proj(ly.silu_mul(F.linear(hs, L["gate_up"])), L["down"])
+            gu = proj(hs, L["gate_up"])
+            if isinstance(gu, ly.SplitProduct):  # silu_mul takes the bf16 product
+                gu = gu.value()
+            x = proj(ly.silu_mul(gu), L["down"])
         out = ly.add_rmsnorm(x, residual, self.norm, s.eps)
         return out.reshape(B, Q, s.hidden)
 

@@ -88,13 +88,13 @@ def test_gemm_rows64_splits_and_argument_checks(d3d_lib):
     assert lib.d3d_gemm_rows64_splits(12288, 2048) == 1
     assert lib.d3d_gemm_rows64_splits(6144, 4096) == 2
     assert lib.d3d_gemm_rows64_splits(2000, 2048) == 1 and lib.d3d_gemm_rows64_splits(2048, 100) == 1
-    # layers.project takes the kernel only on grids of 256 or 512 workgroups
+    # layers.project takes the kernel on grids of 128 to 256 workgroups and of 512
     from d3d_amd import layers as ly
     routed = {(N, K): ly.rows64_splits(N, K) for N, K in ((6144, 4096), (4096, 4096), (24576, 4096),
                                                           (4096, 12288), (4096, 2048), (2048, 2048),
                                                           (12288, 2048), (2048, 6144), (2000, 2048))}
-    assert routed == {(6144, 4096): 0, (4096, 4096): 4, (24576, 4096): 0, (4096, 12288): 8, (4096, 2048): 4,
-                      (2048, 2048): 8, (12288, 2048): 0, (2048, 6144): 8, (2000, 2048): 0}
+    assert routed == {(6144, 4096): 2, (4096, 4096): 4, (24576, 4096): 0, (4096, 12288): 8, (4096, 2048): 4,
+                      (2048, 2048): 8, (12288, 2048): 1, (2048, 6144): 8, (2000, 2048): 0}
     null = ctypes.c_void_p(0)
     dummy = ctypes.c_void_p(256)
     for M, N, K, s in ((0, 64, 128, 1), (65, 64, 128, 1), (8, 100, 128, 1), (8, 64, 100, 1), (8, 64, 128, 2),

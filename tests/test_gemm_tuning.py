@@ -46,8 +46,8 @@ def test_step_shapes_leave_out_what_runs_on_the_hip_gemm():
     got = gemm_tuning.step_gemm_shapes(QWEN3_8B, D3D_1P7B, batches=(4,), anchors=(1,))
     V = QWEN3_8B.vocab
     assert got == sorted([
-        (64, 6144, 4096), (64, 24576, 4096), (64, V, 4096),           # target qkv, gate-up, LM head
-        (64, 12288, 2048), (64, V, 2048),                              # draft recovery gate-up, LM head
+        (64, 24576, 4096), (64, V, 4096),                              # target gate-up, LM head
+        (64, V, 2048),                                                 # draft recovery LM head
         (1088, 4096, 2048), (1088, 2048, 2048), (1088, 12288, 2048),   # packed predict: 4 x 272 rows
         (1088, 2048, 6144), (1088, V, 2048),
     ])

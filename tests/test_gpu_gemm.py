@@ -8,7 +8,9 @@
   of K products in any order -- so a misplaced tile or a stale stage fails,
   while the kernel's own summation order passes.
 * Every split count gives the same product to fp32 rounding, and the splits
-  of a given count always sum to the same bits.
+  of a given count always sum to the same bits; k-step counts outside the
+  register-staged kernel's unrolled set (the direct-to-LDS kernel) meet the
+  same bound.
 * d3d_add_rmsnorm_parts and d3d_qk_rope_append_parts equal the bf16 kernels
   fed bf16(sum of the splits in order) -- the SplitProduct's value -- bit for
   bit, residual and cache included.
@@ -91,6 +93,25 @@ def test_every_split_count_agrees(N, K):
         _within(total, rb)
 
 
+@pytest.mark.parametrize("K,splits", [(640, 1), (1280, 1), (1280, 2), (128 * 7 * 4, 4), (128 * 48, 1)])
+@pytest.mark.parametrize("M", [1, 37, 64])
+def test_step_counts_outside_the_unrolled_set(K, splits, M):
+    """k-step counts per split (5, 10, 7, 48) that the register-staged kernel
+    is not unrolled for run on the direct-to-LDS kernel: same bound."""
+    lib = _lib.load()
+    N = 256
+    x, w = _operands(M, N, K, seed=K + splits + M)
+    st = torch.cuda.current_stream(DEV).cuda_stream
+    if splits == 1:
+        y = torch.empty(M, N, dtype=BF, device=DEV)
+        assert lib.d3d_gemm_rows64(x.data_ptr(), w.data_ptr(), y.data_ptr(), None, M, N, K, 1, st) == 0
+    else:
+        parts = torch.empty(splits, M, N, dtype=torch.float32, device=DEV)
+        assert lib.d3d_gemm_rows64(x.data_ptr(), w.data_ptr(), None, parts.data_ptr(), M, N, K, splits, st) == 0
+        y = ly.SplitProduct(parts, splits).value()
+    _within(y, _reference(x, w))
+
+
 def test_split_sum_kernels_equal_bf16_path():
     T, H = 64, 4096
     g = torch.Generator(device=DEV).manual_seed(3)
@@ -134,9 +155,11 @@ def test_project_falls_back_beyond_64_rows_and_odd_shapes():
     assert isinstance(y, torch.Tensor) and torch.equal(y, F.linear(x, w))
     x2, w2 = _operands(16, 2000, 2048, seed=6)  # N not a multiple of 64
     assert torch.equal(ly.project(x2, w2), F.linear(x2, w2))
-    # grids other than one or two workgroups per CU go to hipBLASLt
-    x3, w3 = _operands(64, 6144, 4096, seed=7)  # 96 tiles x 2 splits
+    # a round and a half of workgroups goes to hipBLASLt
+    x3, w3 = _operands(64, 24576, 4096, seed=7)  # 384 tiles x 1 split
     assert torch.equal(ly.project(x3, w3), F.linear(x3, w3))
+    x6, w6 = _operands(64, 6144, 4096, seed=9)  # 96 tiles x 2 splits: the HIP GEMM
+    assert isinstance(ly.project(x6, w6), ly.SplitProduct)
     x4, w4 = _operands(64, 2048, 6144, seed=8)  # 32 tiles x 8 splits
     assert isinstance(ly.project(x4, w4), ly.SplitProduct)
     # a contiguous view 2 bytes off 16-byte alignment
