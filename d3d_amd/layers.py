@@ -63,12 +63,13 @@ def rows64_splits(N: int, K: int) -> int:
 
     The kernel holds two workgroups per CU (256 CUs); its grid is N / 64
     column tiles times the splits.  Grids of 128 to 256 workgroups and of
-    exactly 512 beat hipBLASLt on every 64-row projection of both models
-    (graph-replayed, HBM-resident weights): the 6144 x 4096 target qkv at
-    192 workgroups 16.6 against 18.2 us, the 12288 x 2048 draft gate-up at
-    192 14.8 against 17.2 us.  A round and a half (the 24576 x 4096 target
-    gate-up at 384: 48.0 against 46.9 us) and smaller grids stay with
-    hipBLASLt.
+    exactly 512 are at least even with hipBLASLt on every 64-row projection
+    of both models (graph-replayed, HBM-resident weights): the 6144 x 4096
+    target qkv at 192 workgroups 16.6 against 17.5-18.3 us, the 12288 x 2048
+    draft gate-up at 192 14.8-16.2 against 15.7 us on its tuned library
+    solution and 17.2-18.2 on the default one.  A round and a half (the
+    24576 x 4096 target gate-up at 384: 48.0 against 46.9 us) and smaller
+    grids stay with hipBLASLt.
     """
     if N % 64 or K % 128:
         return 0
