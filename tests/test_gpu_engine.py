@@ -193,6 +193,56 @@ def test_predict_and_verify_surfaces():
     assert eng.target.free_pages == eng.target.kv.num_pages and eng.draft.free_pages == eng.draft.kv.num_pages
 
 
+def test_prepared_block_inputs_are_used_only_while_they_hold():
+    """Runner.prepare fills a step's block inputs ahead of its forward: a
+    verify and a packed prediction on prepared inputs equal the same calls
+    without them, and after a prefix moves (or a table is trimmed) the
+    forward prepares again instead of using the stale inputs."""
+    from d3d_amd.model import Sequence
+    eng = _engine(23)
+    g = torch.Generator().manual_seed(11)
+    seqs = []
+    for i, n in enumerate((19, 40, 26)):
+        s = Sequence(i, torch.randint(0, 999, (n,), generator=g).tolist())
+        s.prefix = n
+        s.needs_fast_seed = False
+        s.recoveries = 0
+        seqs.append(s)
+    anchors = eng.target.prefill(seqs)
+    eng.draft.prefill(seqs)
+    for s, a in zip(seqs, anchors):
+        s.anchor = a
+    eng._recover(seqs)
+    blocks = [list(s.current) for s in seqs]
+
+    def verify():
+        out = eng.target.verify(seqs, blocks)
+        eng.target.stream.synchronize()
+        return out.tolist()
+
+    def predict():
+        return eng._predict(seqs)
+
+    plain_v, plain_p = verify(), predict()
+    eng._prepare_next(seqs)
+    assert verify() == plain_v and predict() == plain_p
+    # stale: the prefixes move after the preparation (the engine's trim and
+    # next reserve happen in between), so both forwards prepare again
+    eng._prepare_next(seqs)
+    for s in seqs:
+        s.prefix += 1
+        eng.target.trim(s, s.prefix)
+        eng.draft.trim(s, s.prefix)
+    moved_v, moved_p = verify(), predict()
+    eng._prepare_next(seqs)
+    assert verify() == moved_v and predict() == moved_p
+    assert moved_v != plain_v or moved_p != plain_p
+    for s in seqs:
+        eng.target.release(s)
+        eng.draft.release(s)
+    assert eng.target.free_pages == eng.target.kv.num_pages and eng.draft.free_pages == eng.draft.kv.num_pages
+
+
 def test_generic_mask_builder_equals_descriptor():
     """Runner.forward compiles a plain mask callable (the reference's
     Engine._mask closure) to the same per-query visibility the engine's
