@@ -88,6 +88,7 @@ SIGNATURES = {
     "d3d_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "d3d_gemm_rows64": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "d3d_gemm_rows64_splits": (_I, [_I, _I]),
+    "d3d_gemm_rows64_silu_mul": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "d3d_add_rmsnorm_parts": (_I, [_P, _I, _P, _P, _P, _I, _I, _F, _P]),
     "d3d_qk_rope_append_parts": (
         _I,

@@ -161,7 +161,15 @@ __global__ __launch_bounds__(NT) void gemm_rows64_dma_kernel(const uint16_t* __r
 // Register-staged form of the kernel above (same tiles, LDS layout and
 // results): stage st of a lane is rw / rx[st % 2] until it is stored to
 // LDS buffer st % 2; the loads of stage st + 2 then reuse those registers.
-template <int STEPS>
+//
+// SILU: W is a gate-up weight [2 H, K] (gate rows, then up rows) and Y
+// [M, H] = silu(bf16(X Wg^T)) * bf16(X Wu^T), each product rounded as the
+// bf16 GEMM output would be, then evaluated as d3d_silu_mul does.  Tile t
+// stands for output columns 32 t .. 32 t + 31: tile row 16 w + c is gate
+// row 32 t + 8 w + c (c < 8) or the up row of column 32 t + 8 w + c - 8, so
+// a lane's gate and up products of one column sit in lanes c and c + 8 of
+// its 16-lane row.
+template <int STEPS, bool SILU = false>
 __global__ __launch_bounds__(NT, 2) void gemm_rows64_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ w,
                                                             uint16_t* __restrict__ y, float* __restrict__ parts,
@@ -183,7 +191,12 @@ __global__ __launch_bounds__(NT, 2) void gemm_rows64_kernel(const uint16_t* __re
     for (int j = 0; j < LPW; ++j) {
         const int r = (wv * LPW + j) * RPI + lr;
         const int q = lc ^ (r & 7);
-        wsrc[j] = w + (size_t)(n0 + r) * K + kb + 8 * q;
+        int wrow = n0 + r;
+        if constexpr (SILU) {
+            const int col = 32 * blockIdx.x + 8 * (r >> 4) + (r & 7);
+            wrow = (r & 8) ? N / 2 + col : col;
+        }
+        wsrc[j] = w + (size_t)wrow * K + kb + 8 * q;
         xsrc[j] = x + (size_t)min(r, M - 1) * K + kb + 8 * q;
         lofs[j] = r * ROWB + lc * 16;
     }
@@ -215,7 +228,23 @@ __global__ __launch_bounds__(NT, 2) void gemm_rows64_kernel(const uint16_t* __re
         __syncthreads();
         mma_step(buf, acc, wv, c16, g4);
     }
-    store_tile(acc, y, parts, M, N, n0 + 16 * wv + c16, g4);
+    if constexpr (SILU) {
+        const int H = N / 2, col = 32 * blockIdx.x + 8 * wv + (c16 & 7);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float mine = acc[t][r], other = __shfl_xor(mine, 8, kWave);
+                const int m = 16 * t + 4 * g4 + r;
+                if (c16 < 8 && m < M) {
+                    const float gv = bf16_bits_to_f32(f32_to_bf16_bits(mine));
+                    const float uv = bf16_bits_to_f32(f32_to_bf16_bits(other));
+                    y[(size_t)m * H + col] = __builtin_bit_cast(uint16_t, (__bf16)(gv / (1.0f + expf(-gv)) * uv));
+                }
+            }
+    } else {
+        store_tile(acc, y, parts, M, N, n0 + 16 * wv + c16, g4);
+    }
 }
 
 }  // namespace gemm
@@ -238,6 +267,33 @@ extern "C" int d3d_gemm_rows64_splits(int N, int K) {
            K / (2 * s) >= 2 * gemm::TK && (K >= 8192 || (int64_t)2 * s * N <= 16384))
         s *= 2;
     return s;
+}
+
+extern "C" int d3d_gemm_rows64_silu_mul(const void* x, const void* w_gate_up, void* y, int M, int H, int K,
+                                        void* stream) {
+    if (M < 1 || M > 64 || H < 32 || H % 32 || K < gemm::TK || K % gemm::TK) return D3D_E_SHAPE;
+    if (!x || !w_gate_up || !y) return D3D_E_NULL;
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w_gate_up) % 16) return D3D_E_UNSUPPORTED;
+    const dim3 grid(H / 32), block(gemm::NT);
+    const size_t lds = gemm::ST * gemm::STAGEB;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    const uint16_t* wp = static_cast<const uint16_t*>(w_gate_up);
+    uint16_t* yp = static_cast<uint16_t*>(y);
+    switch (K / gemm::TK) {
+#define D3D_ROWS64_SILU(n)                                                                                      \
+    case n:                                                                                                    \
+        hipLaunchKernelGGL((gemm::gemm_rows64_kernel<n, true>), grid, block, lds, s, xp, wp, yp, nullptr, M, 2 * H, K, \
+                           K);                                                                                 \
+        break;
+        D3D_ROWS64_SILU(8) D3D_ROWS64_SILU(16) D3D_ROWS64_SILU(24) D3D_ROWS64_SILU(32) D3D_ROWS64_SILU(48)
+        D3D_ROWS64_SILU(64)
+#undef D3D_ROWS64_SILU
+        default:
+            return D3D_E_UNSUPPORTED;
+    }
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? D3D_OK : (int)err;
 }
 
 extern "C" int d3d_gemm_rows64(const void* x, const void* w, void* y, float* parts, int M, int N, int K,

@@ -109,6 +109,36 @@ def project(x: torch.Tensor, weight: torch.Tensor) -> Product:
     return SplitProduct(parts, splits)
 
 
+def rows64_silu_ok(H: int, K: int) -> bool:
+    """Whether gate_up_silu runs the fused d3d_gemm_rows64_silu_mul for a
+    gate-up weight [2H, K] (its grid is 2H / 64 workgroups; the same grids
+    as rows64_splits, and the step counts the kernel is built for)."""
+    grid = 2 * H // 64
+    return H % 32 == 0 and K % 128 == 0 and K // 128 in (8, 16, 24, 32, 48, 64) and (128 <= grid <= 256 or grid == 512)
+
+
+def gate_up_silu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """silu_mul(F.linear(x, weight)) for bf16 x [M, K] and a gate-up weight
+    [2H, K] (gate rows, then up rows), the MLP's gate_up_proj + SiluAndMul.
+
+    Blocks of at most 64 rows whose shape rows64_silu_ok accepts run one
+    fused launch (d3d_gemm_rows64_silu_mul), equal bit for bit to
+    d3d_gemm_rows64 followed by silu_mul; others run F.linear (hipBLASLt)
+    and silu_mul."""
+    M, K = x.shape
+    H = weight.shape[0] // 2
+    if (M > ROWS64 or weight.shape[0] % 2 or not rows64_silu_ok(H, K) or x.dtype != torch.bfloat16
+            or weight.dtype != torch.bfloat16 or not x.is_contiguous() or not weight.is_contiguous()
+            or x.data_ptr() % 16 or weight.data_ptr() % 16 or weight.shape[1] != K):
+        return silu_mul(F.linear(x, weight))
+    dev = _lib.require_device(x, weight)
+    y = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+    st = _lib.load().d3d_gemm_rows64_silu_mul(x.data_ptr(), weight.data_ptr(), y.data_ptr(), M, H, K,
+                                              _lib.stream_ptr(dev))
+    _lib.check(st, "d3d_gemm_rows64_silu_mul")
+    return y
+
+
 def _bf16_rows(t: torch.Tensor, name: str) -> None:
     if t.dtype != torch.bfloat16 or not t.is_contiguous():
         raise ValueError(f"{name} must be a contiguous bf16 tensor")

@@ -218,10 +218,11 @@ class Qwen3PagedModel(torch.nn.Module):
         attention, O GEMM, fused add + RMSNorm, gate-up GEMM, fused SiLU-mul,
         down GEMM (the decoder layer of serving/vendor/ssd/models/qwen3.py).
         Blocks of at most 64 tokens run the projections on the
-        weight-streaming HIP GEMM where layers.project picks it (when
-        ``rows64_gemm``: the QKV, O and down GEMMs, whose K-split partials the
-        next fused kernel sums, and the draft's gate-up); the target's gate-up
-        and larger blocks use F.linear.
+        weight-streaming HIP GEMM where layers.project / gate_up_silu pick it
+        (when ``rows64_gemm``: the QKV, O and down GEMMs, whose K-split
+        partials the next fused kernel sums, and the draft's gate-up with the
+        SiLU-mul fused in); the target's gate-up and larger blocks use
+        F.linear.
         """
         B, Q = ids.shape
         s = self.shape
@@ -244,10 +245,8 @@ class Qwen3PagedModel(torch.nn.Module):
                                           q_vis, max_seqlen_k=max_context)
             x = proj(o.reshape(B * Q, Hq * d), L["o"])
             ly.add_rmsnorm(x, residual, L["ln2"], s.eps, out=hs)
-            gu = proj(hs, L["gate_up"])
-            if isinstance(gu, ly.SplitProduct):  # silu_mul takes the bf16 product
-                gu = gu.value()
-            x = proj(ly.silu_mul(gu), L["down"])
+            act = ly.gate_up_silu(hs, L["gate_up"]) if self.rows64_gemm else ly.silu_mul(F.linear(hs, L["gate_up"]))
+            x = proj(act, L["down"])
         out = ly.add_rmsnorm(x, residual, self.norm, s.eps)
         return out.reshape(B, Q, s.hidden)
 

@@ -493,6 +493,19 @@ int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* stream);
 int d3d_gemm_rows64(const void* x, const void* w, void* y, float* parts, int M, int N, int K, int splits,
                     void* stream);
 
+/*
+ * The decoder layer's gate-up projection and SiluAndMul in one launch for a
+ * block of at most 64 rows (Qwen3MLP.forward, serving/vendor/ssd/models/
+ * qwen3.py:139-142: gate_up_proj, then act_fn = SiluAndMul,
+ * serving/vendor/ssd/layers/activation.py:6-14): y [M, H] bf16 =
+ * silu(g) * u, where g and u are the bf16-rounded products X Wg^T and
+ * X Wu^T of w_gate_up [2H, K] = [gate rows | up rows] -- the values
+ * d3d_gemm_rows64 (one split) followed by d3d_silu_mul give, bit for bit.
+ * 1 <= M <= 64, H a multiple of 32, K / 128 in {8, 16, 24, 32, 48, 64}
+ * (D3D_E_UNSUPPORTED otherwise), X and W 16-byte aligned.
+ */
+int d3d_gemm_rows64_silu_mul(const void* x, const void* w_gate_up, void* y, int M, int H, int K, void* stream);
+
 /* The split count d3d_gemm_rows64 is fastest with for an [N, K] weight (1 when N or K
  * is not a multiple of 64 or 128). */
 int d3d_gemm_rows64_splits(int N, int K);

@@ -97,6 +97,11 @@ def test_gemm_rows64_splits_and_argument_checks(d3d_lib):
                       (2048, 2048): 8, (12288, 2048): 1, (2048, 6144): 8, (2000, 2048): 0}
     null = ctypes.c_void_p(0)
     dummy = ctypes.c_void_p(256)
+    # the fused gate-up + SiLU-mul: shape, step-count and pointer checks before any launch
+    for M, H, K in ((0, 64, 1024), (65, 64, 1024), (8, 48, 1024), (8, 64, 1000), (8, 64, 1152)):
+        assert lib.d3d_gemm_rows64_silu_mul(dummy, dummy, dummy, M, H, K, null) in (-1, -5), (M, H, K)
+    assert lib.d3d_gemm_rows64_silu_mul(dummy, dummy, dummy, 8, 64, 1152, null) == -5  # 9 steps: D3D_E_UNSUPPORTED
+    assert lib.d3d_gemm_rows64_silu_mul(null, dummy, dummy, 8, 64, 1024, null) == -4
     for M, N, K, s in ((0, 64, 128, 1), (65, 64, 128, 1), (8, 100, 128, 1), (8, 64, 100, 1), (8, 64, 128, 2),
                        (8, 64, 4096, 3), (8, 64, 4096, 32)):
         assert lib.d3d_gemm_rows64(dummy, dummy, dummy, dummy, M, N, K, s, null) == -1, (M, N, K, s)

@@ -11,6 +11,8 @@
   of a given count always sum to the same bits; k-step counts outside the
   register-staged kernel's unrolled set (the direct-to-LDS kernel) meet the
   same bound.
+* d3d_gemm_rows64_silu_mul equals d3d_gemm_rows64 followed by silu_mul bit
+  for bit.
 * d3d_add_rmsnorm_parts and d3d_qk_rope_append_parts equal the bf16 kernels
   fed bf16(sum of the splits in order) -- the SplitProduct's value -- bit for
   bit, residual and cache included.
@@ -110,6 +112,28 @@ def test_step_counts_outside_the_unrolled_set(K, splits, M):
         assert lib.d3d_gemm_rows64(x.data_ptr(), w.data_ptr(), None, parts.data_ptr(), M, N, K, splits, st) == 0
         y = ly.SplitProduct(parts, splits).value()
     _within(y, _reference(x, w))
+
+
+@pytest.mark.parametrize("H,K", [(6144, 2048), (12288, 4096), (256, 1024)])
+@pytest.mark.parametrize("M", [1, 5, 37, 64])
+def test_fused_gate_up_silu_equals_the_two_kernels(H, K, M):
+    """d3d_gemm_rows64_silu_mul equals d3d_gemm_rows64 (one split) on the
+    gate-up weight followed by silu_mul, bit for bit, and the product stays
+    within the exact-product bound."""
+    lib = _lib.load()
+    x, w = _operands(M, 2 * H, K, seed=H + K + M)
+    st = torch.cuda.current_stream(DEV).cuda_stream
+    gu = torch.empty(M, 2 * H, dtype=BF, device=DEV)
+    assert lib.d3d_gemm_rows64(x.data_ptr(), w.data_ptr(), gu.data_ptr(), None, M, 2 * H, K, 1, st) == 0
+    want = ly.silu_mul(gu)
+    got = torch.empty(M, H, dtype=BF, device=DEV)
+    assert lib.d3d_gemm_rows64_silu_mul(x.data_ptr(), w.data_ptr(), got.data_ptr(), M, H, K, st) == 0
+    assert torch.equal(got, want)
+    _within(gu, _reference(x, w))
+    if ly.rows64_silu_ok(H, K):
+        assert torch.equal(ly.gate_up_silu(x, w), want)
+    else:
+        assert torch.equal(ly.gate_up_silu(x, w), ly.silu_mul(F.linear(x, w)))
 
 
 def test_split_sum_kernels_equal_bf16_path():
