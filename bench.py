@@ -256,6 +256,35 @@ class GemmStep(_Bound):
             torch.mm(self.x, self.w.t(), out=self.y)
 
 
+class SiluStep(_Bound):
+    """Pre-bound 64-row gate-up projection plus SiLU-mul: the fused
+    d3d_gemm_rows64_silu_mul, or hipBLASLt (torch.mm) then d3d_silu_mul."""
+
+    def __init__(self, M, N, K, dev, fused: bool, seed=0):
+        from d3d_amd import _lib
+        self.lib = _lib.load()
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        self.w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        self.gu = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        self.y = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
+        self.fused, self.shape = fused, (M, N // 2, K)
+        self.args = (torch.cuda.current_stream(dev).cuda_stream,)
+        self._check = _lib.check
+        self.bytes = N * K * 2 + M * K * 2 + M * (N // 2) * 2
+
+    def __call__(self):
+        M, H, K = self.shape
+        if self.fused:
+            st = self.lib.d3d_gemm_rows64_silu_mul(self.x.data_ptr(), self.w.data_ptr(), self.y.data_ptr(), M, H, K,
+                                                   self.args[-1])
+        else:
+            torch.mm(self.x, self.w.t(), out=self.gu)
+            st = self.lib.d3d_silu_mul(self.gu.data_ptr(), self.y.data_ptr(), M, H, self.args[-1])
+        if st:
+            self._check(st, "gate-up + SiLU-mul")
+
+
 # The 64-row projections of the two models (N, K): qkv, o, gate-up, down.
 GEMM_SHAPES = {
     "target qkv": (6144, 4096), "target o": (4096, 4096), "target gate_up": (24576, 4096),
@@ -284,6 +313,14 @@ def gemm_rows64_bench(dev, calls: int):
                 row["splits"] = r.calls[0].splits
             del r
             torch.cuda.empty_cache()
+        if name.endswith("gate_up"):
+            # the gate-up with its SiLU-mul: fused launch against hipBLASLt + d3d_silu_mul
+            row["silu_fused_route"] = ly.rows64_silu_ok(N // 2, K)
+            for fused in (True, False):
+                r = Rotating(lambda i: SiluStep(64, N, K, dev, fused, seed=i), N * K * 2)
+                row[("fused_silu" if fused else "hipblaslt_silu") + "_us"] = round(time_graph(r, calls, warm, dev) * 1e3, 2)
+                del r
+                torch.cuda.empty_cache()
         out.append(row)
     return out
 
