@@ -180,17 +180,18 @@ class Runner:
         block_inputs(self.kv, seqs, self.name, [s.prefix for s in seqs], Q, self.device, width, out=step.inputs())
         return step
 
-    def prepare(self, seqs: List[Sequence], Q: int, *, mask_builder=None, topk: int = 0) -> None:
+    def prepare(self, seqs: List[Sequence], Q: int, *, mask_builder=None, topk: int = 0,
+                deferred: bool = False) -> None:
         """Fill the page tables, slots and context lengths of the next block
         forward over ``seqs`` (Q tokens at their prefixes) ahead of it, on
         the runner's stream, so that the forward itself only copies its
-        token ids and replays.  The next ``forward`` / ``verify`` with the
-        same requests, prefixes, page lists and block shape uses them;
-        anything else prepares again."""
+        token ids and replays.  The next ``forward`` / ``verify`` (or, with
+        ``deferred``, ``forward_deferred``) with the same requests, prefixes,
+        page lists and block shape uses them; anything else prepares again."""
         with torch.cuda.stream(self.stream):
             if self.draft:
                 vis = self._visibility(seqs, Q, mask_builder)
-                step = self._prepare(seqs, Q, "forward", vis, topk)
+                step = self._prepare(seqs, Q, "hidden" if deferred else "forward", vis, 0 if deferred else topk)
             else:
                 step = self._prepare(seqs, Q, "verify", None, 0)
             step.prepared = tuple((s.seq_id, s.prefix, tuple(self.table(s))) for s in seqs)
@@ -203,6 +204,9 @@ class Runner:
                 def post(hidden, ids):
                     out = ss.greedy_accept(self.model.logits(hidden), ids)
                     return out.accepted, out.out_token
+            elif kind == "hidden":
+                def post(hidden, ids):
+                    return hidden
             else:
                 def post(hidden, ids):
                     top = topk_tokens(self.model.logits(hidden), max(k, 1))
@@ -229,6 +233,35 @@ class Runner:
             if topk:
                 return copy(top[..., :topk].contiguous()), copy(greedy)
             return copy(greedy)
+
+    @torch.inference_mode()
+    def forward_deferred(self, seqs: List[Sequence], tokens, *, positions=None, mask_builder=None, topk: int = 1,
+                         post_stream: torch.cuda.Stream):
+        """``forward(..., topk=topk, host=True)`` with the LM head and the
+        top-k moved to ``post_stream``: the block forward replays on this
+        runner's stream; the logits and their top-k run on ``post_stream``
+        once it has finished.  Returns (top, greedy, done): pinned host
+        tensors valid once the event ``done`` (recorded on ``post_stream``)
+        has completed.  The engine defers its packed prediction's LM head
+        onto the target's stream this way: queued behind the verify, it runs
+        while the draft stream does the recovery, not inside the verify."""
+        if topk < 1:
+            raise ValueError("forward_deferred needs topk >= 1")
+        with torch.cuda.stream(self.stream):
+            ids = _host_ids(tokens)
+            B, Q = ids.shape
+            vis = self._visibility(seqs, Q, mask_builder) if self.draft else None
+            step = self._prepare(seqs, Q, "hidden", vis, 0)
+            hidden = step.run(ids, None if positions is None else _host_ids(positions))
+            ready = torch.cuda.Event()
+            ready.record(self.stream)
+        with torch.cuda.stream(post_stream):
+            post_stream.wait_event(ready)
+            top = topk_tokens(self.model.logits(hidden), topk)
+            out = _to_host(top[..., :topk].contiguous()), _to_host(top[..., 0])
+            done = torch.cuda.Event()
+            done.record(post_stream)
+        return out[0], out[1], done
 
     @torch.inference_mode()
     def verify(self, seqs: List[Sequence], tokens) -> torch.Tensor:

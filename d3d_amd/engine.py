@@ -31,7 +31,10 @@ The reference runs the target in another process on another GPU
 both models are co-resident, each Runner on its own HIP stream (its own
 hardware queue), so the target's verify and the draft's packed prediction
 overlap, and the exchange is a pair of stream events plus small pinned
-device-to-host copies.  Verify fuses the greedy acceptance kernel after
+device-to-host copies.  The packed prediction's LM head and top-k are queued
+on the target's stream behind the verify, so they run beside the recovery
+forward (which needs the prediction's K/V, not its tokens) instead of
+inside the verify.  Verify fuses the greedy acceptance kernel after
 the target forward (commit length and anchor come back, not the posterior
 list); its results equal Engine._accepted on the posterior.
 """
@@ -239,7 +242,7 @@ class Engine:
         Q = K + len(layout) * K
         for off in range(0, len(seqs), self.micro):
             group = seqs[off:off + self.micro]
-            self.draft.prepare(group, Q, mask_builder=self._mask([layout] * len(group)), topk=A + 1)
+            self.draft.prepare(group, Q, mask_builder=self._mask([layout] * len(group)), deferred=True)
 
     def _fast_backup(self, seqs: List[Sequence]) -> None:
         """serving/engine.py:64-71: a random block after the anchor (greedy
@@ -291,21 +294,24 @@ class Engine:
                 for j, (_, a) in enumerate(specs[b]):
                     if a is not None:
                         ids[b, K + j * K] = a
-            top, greedy = self.draft.forward(group, torch.from_numpy(ids), positions=torch.from_numpy(pos),
-                                             mask_builder=self._mask(specs), topk=A + 1, host=True)
-            pending.append((group, specs, top, greedy))
+            # The block forward runs on the draft stream; its LM head and
+            # top-(A+1) are queued on the target stream, behind the verify,
+            # so that they run beside the recovery rather than inside the
+            # verify (the recovery needs the forward's K/V, not its tokens).
+            top, greedy, done = self.draft.forward_deferred(
+                group, torch.from_numpy(ids), positions=torch.from_numpy(pos), mask_builder=self._mask(specs),
+                topk=A + 1, post_stream=self.target.stream)
+            pending.append((group, specs, top, greedy, done))
         return pending
 
-    def _predict_collect(self, pending, done: Optional[torch.cuda.Event] = None) -> Dict[int, Dict]:
-        """The packed predictions as host lists, once the draft stream has
-        drained (or once ``done``, an event recorded after them, has)."""
-        if done is None:
-            self.draft.stream.synchronize()
-        else:
-            done.synchronize()
+    def _predict_collect(self, pending) -> Dict[int, Dict]:
+        """The packed predictions as host lists, once their top-k copies
+        (on the target stream) have completed."""
+        for entry in pending:
+            entry[4].synchronize()
         K = self.K
         results: Dict[int, Dict] = {}
-        for group, specs, top, greedy in pending:
+        for group, specs, top, greedy, _ in pending:
             top_l, greedy_l = top.tolist(), greedy.tolist()
             for b, s in enumerate(group):
                 outcomes = {}
@@ -428,11 +434,12 @@ class Engine:
             ev["ps"].record(self.draft.stream)
             pending = self._side("draft", self._predict_submit, running)
             ev["pe"].record(self.draft.stream)
-            # The verify result decides the step; the predictions are read
-            # once the recovery forwards are queued behind them.
-            self._side("target", self.target.stream.synchronize)
+            # The verify result decides the step (the predictions' top-k is
+            # queued behind it on the same stream); the predictions are read
+            # once the recovery forwards are queued.
+            self._side("target", ev["ve"].synchronize)
             accepted = list(zip(*res.tolist()))
-            predicted = {s.seq_id: set(specs[b]) for group, specs, _, _ in pending for b, s in enumerate(group)}
+            predicted = {s.seq_id: set(e[1][b]) for e in pending for b, s in enumerate(e[0])}
             steps += 1
             remaining, recover, hits = [], [], []
             for s, block, (n, anchor) in zip(running, blocks, accepted):
@@ -475,9 +482,9 @@ class Engine:
             ev["re"].record(self.draft.stream)
             if running and (exhausted or len(running) >= concurrency):
                 self._side("draft", self._prepare_next, running)
-            # The predictions finished before the verify did: read them
-            # while the recovery forwards run.
-            predictions = self._side("draft", self._predict_collect, pending, ev["pe"])
+            # The predictions' top-k runs beside the recovery forwards:
+            # read them while the recovery finishes.
+            predictions = self._side("draft", self._predict_collect, pending)
             for s, key, anchor in hits:
                 selected = predictions[s.seq_id][key]
                 s.current, s.top = list(selected[0]), selected[1]
