@@ -186,7 +186,7 @@ class Runner:
         forward over ``seqs`` (Q tokens at their prefixes) ahead of it, on
         the runner's stream, so that the forward itself only copies its
         token ids and replays.  The next ``forward`` / ``verify`` (or, with
-        ``deferred``, ``forward_deferred``) with the same requests, prefixes,
+        ``deferred``, ``forward_hidden``) with the same requests, prefixes,
         page lists and block shape uses them; anything else prepares again."""
         with torch.cuda.stream(self.stream):
             if self.draft:
@@ -235,18 +235,12 @@ class Runner:
             return copy(greedy)
 
     @torch.inference_mode()
-    def forward_deferred(self, seqs: List[Sequence], tokens, *, positions=None, mask_builder=None, topk: int = 1,
-                         post_stream: torch.cuda.Stream):
-        """``forward(..., topk=topk, host=True)`` with the LM head and the
-        top-k moved to ``post_stream``: the block forward replays on this
-        runner's stream; the logits and their top-k run on ``post_stream``
-        once it has finished.  Returns (top, greedy, done): pinned host
-        tensors valid once the event ``done`` (recorded on ``post_stream``)
-        has completed.  The engine defers its packed prediction's LM head
-        onto the target's stream this way: queued behind the verify, it runs
-        while the draft stream does the recovery, not inside the verify."""
-        if topk < 1:
-            raise ValueError("forward_deferred needs topk >= 1")
+    def forward_hidden(self, seqs: List[Sequence], tokens, *, positions=None, mask_builder=None):
+        """The block forward of ``forward`` without its LM head: returns the
+        final hidden states [B, Q, hidden] (a captured step's output, valid
+        until the next forward of that shape) and an event recorded on this
+        runner's stream after them.  ``topk_post`` turns any of its rows into
+        tokens later, on any stream."""
         with torch.cuda.stream(self.stream):
             ids = _host_ids(tokens)
             B, Q = ids.shape
@@ -255,12 +249,22 @@ class Runner:
             hidden = step.run(ids, None if positions is None else _host_ids(positions))
             ready = torch.cuda.Event()
             ready.record(self.stream)
-        with torch.cuda.stream(post_stream):
-            post_stream.wait_event(ready)
-            top = topk_tokens(self.model.logits(hidden), topk)
+        return hidden, ready
+
+    @torch.inference_mode()
+    def topk_post(self, rows: torch.Tensor, topk: int, stream: torch.cuda.Stream, after=()):
+        """LM head + top-``topk`` of hidden rows [R, hidden] on ``stream``,
+        once the events ``after`` have completed: pinned host (top [R, topk],
+        greedy [R]) and the event after their copies."""
+        if topk < 1:
+            raise ValueError("topk_post needs topk >= 1")
+        with torch.cuda.stream(stream):
+            for ev in after:
+                stream.wait_event(ev)
+            top = topk_tokens(self.model.logits(rows), topk)
             out = _to_host(top[..., :topk].contiguous()), _to_host(top[..., 0])
             done = torch.cuda.Event()
-            done.record(post_stream)
+            done.record(stream)
         return out[0], out[1], done
 
     @torch.inference_mode()

@@ -31,10 +31,11 @@ The reference runs the target in another process on another GPU
 both models are co-resident, each Runner on its own HIP stream (its own
 hardware queue), so the target's verify and the draft's packed prediction
 overlap, and the exchange is a pair of stream events plus small pinned
-device-to-host copies.  The packed prediction's LM head and top-k are queued
-on the target's stream behind the verify, so they run beside the recovery
-forward (which needs the prediction's K/V, not its tokens) instead of
-inside the verify.  Verify fuses the greedy acceptance kernel after
+device-to-host copies.  The packed prediction keeps its final hidden
+states; once the verify result is known only the branches it hits (one per
+request at most) go through the draft's LM head and top-k, queued on the
+target's stream beside the recovery forward (which needs the prediction's
+K/V, not its tokens).  ``_predict`` still returns every branch.  Verify fuses the greedy acceptance kernel after
 the target forward (commit length and anchor come back, not the posterior
 list); its results equal Engine._accepted on the posterior.
 """
@@ -256,9 +257,11 @@ class Engine:
             s.needs_fast_seed = True
             s.fast_backups += 1
 
-    def _predict_submit(self, seqs: List[Sequence]):
+    def _predict_submit(self, seqs: List[Sequence], lazy: bool = False):
         """serving/engine.py:73-131 up to the packed forwards, which run on
-        the draft stream; returns what _predict_collect needs."""
+        the draft stream; returns what _predict_collect (every branch's
+        tokens) or, with ``lazy``, _predict_hits needs: then no branch is
+        turned into tokens yet, only the hidden states are kept."""
         K, A = self.K, self.A
         missing = [s for s in seqs if s.needs_fast_seed]
         missing_ids = {s.seq_id for s in missing}
@@ -294,15 +297,56 @@ class Engine:
                 for j, (_, a) in enumerate(specs[b]):
                     if a is not None:
                         ids[b, K + j * K] = a
-            # The block forward runs on the draft stream; its LM head and
-            # top-(A+1) are queued on the target stream, behind the verify,
-            # so that they run beside the recovery rather than inside the
-            # verify (the recovery needs the forward's K/V, not its tokens).
-            top, greedy, done = self.draft.forward_deferred(
-                group, torch.from_numpy(ids), positions=torch.from_numpy(pos), mask_builder=self._mask(specs),
-                topk=A + 1, post_stream=self.target.stream)
-            pending.append((group, specs, top, greedy, done))
+            hidden, ready = self.draft.forward_hidden(group, torch.from_numpy(ids), positions=torch.from_numpy(pos),
+                                                      mask_builder=self._mask(specs))
+            if lazy:
+                pending.append((group, specs, hidden, ready))
+                continue
+            # Every branch's tokens: the LM head and top-(A+1) of all rows,
+            # queued on the target stream behind the verify.
+            B_, Q_, H_ = hidden.shape
+            top, greedy, done = self.draft.topk_post(hidden.reshape(B_ * Q_, H_), A + 1, self.target.stream, (ready,))
+            pending.append((group, specs, top.view(B_, Q_, A + 1), greedy.view(B_, Q_), done))
         return pending
+
+    def _predict_hits(self, pending, hits):
+        """The tokens of the predicted branches that matched the verify
+        (``hits``: (sequence, branch key, anchor)), from the lazily kept
+        hidden states of _predict_submit(..., lazy=True): the LM head and
+        top-(A+1) of those K rows per hit only, queued on the target stream
+        behind the verify.  Returns (top, greedy, done, rows) for
+        _apply_hits, or None without hits."""
+        if not hits:
+            return None
+        K = self.K
+        where = {s.seq_id: (e, b) for e in pending for b, s in enumerate(e[0])}
+        rows, after = [], []
+        for s, key, _ in hits:
+            (group, specs, hidden, ready), b = where[s.seq_id]
+            start = K + specs[b].index(key) * K
+            rows.append((hidden, b, start))
+            if ready not in after:
+                after.append(ready)
+        with torch.cuda.stream(self.target.stream):
+            for ev in after:
+                self.target.stream.wait_event(ev)
+            x = torch.cat([h[b, st:st + K] for h, b, st in rows])
+        top, greedy, done = self.draft.topk_post(x, self.A + 1, self.target.stream)
+        return top, greedy, done
+
+    def _apply_hits(self, hits, out) -> None:
+        """s.current, s.top of each hit from _predict_hits' tokens."""
+        if out is None:
+            return
+        top, greedy, done = out
+        done.synchronize()
+        K = self.K
+        top_l, greedy_l = top.tolist(), greedy.tolist()
+        for i, (s, key, anchor) in enumerate(hits):
+            s.current = greedy_l[i * K:(i + 1) * K]
+            s.current[0] = anchor
+            s.top = top_l[i * K:(i + 1) * K]
+            s.hits += 1
 
     def _predict_collect(self, pending) -> Dict[int, Dict]:
         """The packed predictions as host lists, once their top-k copies
@@ -432,11 +476,11 @@ class Engine:
             ev["ve"].record(self.target.stream)
             # ... while the draft predicts every outcome on its own.
             ev["ps"].record(self.draft.stream)
-            pending = self._side("draft", self._predict_submit, running)
+            pending = self._side("draft", self._predict_submit, running, True)
             ev["pe"].record(self.draft.stream)
-            # The verify result decides the step (the predictions' top-k is
-            # queued behind it on the same stream); the predictions are read
-            # once the recovery forwards are queued.
+            # The verify result decides the step; only the branches it hits
+            # are then turned into tokens (their LM head on the target
+            # stream, beside the recovery forwards).
             self._side("target", ev["ve"].synchronize)
             accepted = list(zip(*res.tolist()))
             predicted = {s.seq_id: set(e[1][b]) for e in pending for b, s in enumerate(e[0])}
@@ -473,6 +517,7 @@ class Engine:
             running = remaining
             miss_rounds += bool(recover)
             miss_requests += len(recover)
+            hit_tokens = self._side("draft", self._predict_hits, pending, hits)
             ev["rs"].record(self.draft.stream)
             recovered = []
             if self.backup in ("fast", "fast_legacy"):
@@ -482,14 +527,7 @@ class Engine:
             ev["re"].record(self.draft.stream)
             if running and (exhausted or len(running) >= concurrency):
                 self._side("draft", self._prepare_next, running)
-            # The predictions' top-k runs beside the recovery forwards:
-            # read them while the recovery finishes.
-            predictions = self._side("draft", self._predict_collect, pending)
-            for s, key, anchor in hits:
-                selected = predictions[s.seq_id][key]
-                s.current, s.top = list(selected[0]), selected[1]
-                s.current[0] = anchor
-                s.hits += 1
+            self._side("draft", self._apply_hits, hits, hit_tokens)
             self._side("draft", self.draft.stream.synchronize)
             self._apply_recovered(recovered)
             decode_s += time.perf_counter() - t_step

@@ -193,6 +193,52 @@ def test_predict_and_verify_surfaces():
     assert eng.target.free_pages == eng.target.kv.num_pages and eng.draft.free_pages == eng.draft.kv.num_pages
 
 
+def test_lazy_hit_branches_equal_the_full_prediction():
+    """The engine keeps the packed prediction's hidden states and turns only
+    the branches the verify hits into tokens (_predict_hits): for every
+    branch key of every request, those tokens equal _predict's (every
+    branch through the LM head at once) -- block with the anchor in its
+    first slot, and top-(A+1)."""
+    from d3d_amd.model import Sequence
+    eng = _engine(29, anchor_num=2)
+    g = torch.Generator().manual_seed(13)
+    seqs = []
+    for i, n in enumerate((21, 34, 27)):
+        s = Sequence(i, torch.randint(0, 999, (n,), generator=g).tolist())
+        s.prefix = n
+        s.needs_fast_seed = False
+        s.recoveries = s.hits = 0
+        seqs.append(s)
+    anchors = eng.target.prefill(seqs)
+    eng.draft.prefill(seqs)
+    for s, a in zip(seqs, anchors):
+        s.anchor = a
+    eng._recover(seqs)
+    saved = [(list(s.current), [list(t) for t in s.top]) for s in seqs]
+    full = eng._predict(seqs)
+    pending = eng._predict_submit(seqs, lazy=True)
+    specs = {s.seq_id: e[1][b] for e in pending for b, s in enumerate(e[0])}
+    checked = 0
+    for j in range(2 * 15 + 1):  # every branch position, one key per request each round
+        hits = []
+        for s in seqs:
+            key = specs[s.seq_id][j]
+            hits.append((s, key, key[1] if key[1] is not None else 123))
+        out = eng._predict_hits(pending, hits)
+        eng._apply_hits(hits, out)
+        for (s, key, anchor), (cur, top) in zip(hits, saved):
+            block, want_top = full[s.seq_id][key]
+            want = list(block)
+            want[0] = anchor
+            assert s.current == want and s.top == want_top, (s.seq_id, key)
+            s.current, s.top = list(cur), [list(t) for t in top]
+            checked += 1
+    assert checked == 3 * 31
+    for s in seqs:
+        eng.target.release(s)
+        eng.draft.release(s)
+
+
 def test_prepared_block_inputs_are_used_only_while_they_hold():
     """Runner.prepare fills a step's block inputs ahead of its forward: a
     verify and a packed prediction on prepared inputs equal the same calls
