@@ -332,6 +332,7 @@ def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40,
     synchronisations.  ``blocks`` timed blocks of ``calls`` calls each; the
     median block is returned (the first block of a process can run several
     microseconds per call slower while the GPU settles)."""
+    from d3d_amd import _lib
     s = torch.cuda.Stream(dev)
     for c in r.calls:
         c.bind_stream(s.cuda_stream)
@@ -340,7 +341,7 @@ def time_graph(r: "Rotating", calls: int, warmup: int, dev, per_graph: int = 40,
         for c in r.calls:
             c()
         torch.cuda.synchronize(dev)
-        with torch.cuda.graph(g, stream=s):
+        with _lib.collection_paused(), torch.cuda.graph(g, stream=s):
             for _ in range(per_graph):
                 r()
         for _ in range(max(1, -(-warmup // per_graph))):

@@ -7,6 +7,7 @@ Build it with ``python -m d3d_amd.build``.
 from __future__ import annotations
 
 import ctypes
+import gc
 from pathlib import Path
 from typing import Optional
 
@@ -158,22 +159,48 @@ _workspaces: dict = {}
 _capture_owner: Optional[list] = None
 
 
+class collection_paused:
+    """Python's cyclic garbage collector stays off inside (its previous
+    state is restored on exit; nesting is fine).
+
+    Graph captures run under it.  A collection that an allocation starts in
+    the middle of a capture runs the finalizers of whatever unreachable
+    objects exist -- an earlier step's graph, events, pinned buffers -- and
+    their HIP calls are not allowed while a stream captures; an error raised
+    in a finalizer aborts the process.  torch.cuda.graph no longer collects
+    before it begins a capture, so the garbage is left for a collection
+    after the capture instead."""
+
+    def __enter__(self):
+        self.was_enabled = gc.isenabled()
+        gc.disable()
+        return self
+
+    def __exit__(self, *exc):
+        if self.was_enabled:
+            gc.enable()
+        return False
+
+
 class capture_workspaces:
     """Context for HIP graph capture: workspaces requested inside it are
     allocated afresh and appended to ``owner``, which must live as long as the
-    captured graph (the graph's kernels keep their addresses)."""
+    captured graph (the graph's kernels keep their addresses).  No garbage
+    collection runs inside it (``collection_paused``)."""
 
     def __init__(self, owner: list):
         self.owner = owner
 
     def __enter__(self):
         global _capture_owner
+        self.paused = collection_paused().__enter__()
         self.prev, _capture_owner = _capture_owner, self.owner
         return self.owner
 
     def __exit__(self, *exc):
         global _capture_owner
         _capture_owner = self.prev
+        self.paused.__exit__(*exc)
         return False
 
 

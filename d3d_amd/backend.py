@@ -200,16 +200,21 @@ class Runner:
         key = (kind, B, Q, width, k, None if vis is None else (tuple(vis.shape), vis.numpy().tobytes()))
         step = self._steps.get(key)
         if step is None:
+            # The post functions hold the model, not the runner: a step that
+            # referred back to the runner holding it would make every dropped
+            # runner, with its captured graphs, garbage that only a cyclic
+            # collection frees, at a moment nobody chooses.
+            model = self.model
             if kind == "verify":
                 def post(hidden, ids):
-                    out = ss.greedy_accept(self.model.logits(hidden), ids)
+                    out = ss.greedy_accept(model.logits(hidden), ids)
                     return out.accepted, out.out_token
             elif kind == "hidden":
                 def post(hidden, ids):
                     return hidden
             else:
                 def post(hidden, ids):
-                    top = topk_tokens(self.model.logits(hidden), max(k, 1))
+                    top = topk_tokens(model.logits(hidden), max(k, 1))
                     return top, top[..., 0]
             step = BlockStep(self.model, self.kv, B, Q, width, causal=not self.draft, post=post,
                              use_graph=self.use_graphs, q_vis=vis)

@@ -138,6 +138,29 @@ def test_fast_backups_stay_lossless(backup):
     _same_up_to_near_tie(W, prompts, [o["tokens"] for o in want["outputs"]], [o["tokens"] for o in got["outputs"]])
 
 
+def test_a_dropped_engine_frees_its_graphs_by_reference_counting():
+    """Runners and their captured steps form no reference cycle: dropping
+    an engine frees its graphs at once, with the cyclic collector off, so no
+    collection pass meets them later in the middle of another capture."""
+    import gc
+    import weakref
+    eng = _engine(19)
+    prompts = torch.randint(0, 999, (2, 20), generator=torch.Generator().manual_seed(8)).tolist()
+    eng.generate(prompts, 2, max_new_tokens=8, ignore_eos=True)
+    steps = [st for r in (eng.target, eng.draft) for st in r._steps.values()]
+    assert steps and all(st.graph is not None for st in steps)
+    refs = [weakref.ref(o) for o in (eng, eng.target, eng.draft, *steps)]
+    torch.cuda.synchronize()
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        del steps, eng
+        assert [r() is None for r in refs] == [True] * len(refs)
+    finally:
+        if was_enabled:
+            gc.enable()
+
+
 def test_engines_share_one_dedicated_stream_per_role():
     """Engines built one after another reuse the process's two dedicated
     streams (one hardware queue each) instead of adding two per engine, and

@@ -6,7 +6,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from d3d_amd import gemm_tuning
+from d3d_amd import _lib, gemm_tuning
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -59,7 +59,7 @@ def _graph_replays_check() -> None:
             torch.mm(x, w.t(), out=o)
         torch.cuda.synchronize(DEV)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
+        with _lib.collection_paused(), torch.cuda.graph(g, stream=s):
             for (x, w), o in zip(ops, outs):
                 torch.mm(x, w.t(), out=o)
     for rep in range(4):
