@@ -254,16 +254,18 @@ using namespace d3d;
 
 extern "C" int d3d_gemm_rows64_splits(int N, int K) {
     if (N < gemm::TN || N % gemm::TN || K < gemm::TK || K % gemm::TK) return 1;
-    // The most splits whose grid is one round of resident workgroups (two
-    // per CU with 64 KB of LDS each: 512), leaving every split at least two
-    // k steps, and -- below K = 8192, where more splits buy less -- at most
-    // 16,384 partial floats per output row: the consumer of the product
-    // reads every partial back, about 1 us per 4 MB at 64 rows.  Measured
-    // on the 64-row projections of both models with 1-16 splits, counting
-    // that read, this is within 0.3 us of the fastest count on each.
+    // The most splits whose grid is at most one workgroup per CU (256),
+    // leaving every split at least two k steps, and -- below K = 8192, where
+    // more splits buy less -- at most 16,384 partial floats per output row:
+    // the consumer of the product reads every partial back, about 1 us per
+    // 4 MB at 64 rows.  Measured with that consumer (d3d_add_rmsnorm_parts)
+    // on rotating HBM-resident weights: 4096 x 12288 at 4 splits 27.6 us
+    // against 31.2 at 8 (a full round of two per CU), 4096 x 4096 at 4
+    // splits 14.9 against 17.9 at 8, 2048 x 6144 at 8 splits 13.8 against
+    // 15.4 at 4 and 16.6 at 16.
     const int tiles = N / gemm::TN;
     int s = 1;
-    while (s < gemm::kMaxSplits && tiles * 2 * s <= 512 && K % (gemm::TK * 2 * s) == 0 &&
+    while (s < gemm::kMaxSplits && tiles * 2 * s <= 256 && K % (gemm::TK * 2 * s) == 0 &&
            K / (2 * s) >= 2 * gemm::TK && (K >= 8192 || (int64_t)2 * s * N <= 16384))
         s *= 2;
     return s;

@@ -79,7 +79,7 @@ def test_gemm_rows64_splits_and_argument_checks(d3d_lib):
     lib = d3d_lib
     # one round of 512 resident workgroups, at least two 128-wide k steps per
     # split, at most 16,384 partial floats per row below K = 8192
-    assert lib.d3d_gemm_rows64_splits(4096, 12288) == 8
+    assert lib.d3d_gemm_rows64_splits(4096, 12288) == 4
     assert lib.d3d_gemm_rows64_splits(2048, 2048) == 8
     assert lib.d3d_gemm_rows64_splits(2048, 6144) == 8
     assert lib.d3d_gemm_rows64_splits(4096, 2048) == 4
@@ -93,7 +93,7 @@ def test_gemm_rows64_splits_and_argument_checks(d3d_lib):
     routed = {(N, K): ly.rows64_splits(N, K) for N, K in ((6144, 4096), (4096, 4096), (24576, 4096),
                                                           (4096, 12288), (4096, 2048), (2048, 2048),
                                                           (12288, 2048), (2048, 6144), (2000, 2048))}
-    assert routed == {(6144, 4096): 2, (4096, 4096): 4, (24576, 4096): 0, (4096, 12288): 8, (4096, 2048): 4,
+    assert routed == {(6144, 4096): 2, (4096, 4096): 4, (24576, 4096): 0, (4096, 12288): 4, (4096, 2048): 4,
                       (2048, 2048): 8, (12288, 2048): 1, (2048, 6144): 8, (2000, 2048): 0}
     null = ctypes.c_void_p(0)
     dummy = ctypes.c_void_p(256)
