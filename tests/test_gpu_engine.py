@@ -216,17 +216,19 @@ def test_predict_and_verify_surfaces():
     assert eng.target.free_pages == eng.target.kv.num_pages and eng.draft.free_pages == eng.draft.kv.num_pages
 
 
-def test_lazy_hit_branches_equal_the_full_prediction():
+@pytest.mark.parametrize("lens,every", [((21, 34, 27), 1), ((21, 34, 27, 40, 18, 25), 2)])
+def test_lazy_hit_branches_equal_the_full_prediction(lens, every):
     """The engine keeps the packed prediction's hidden states and turns only
     the branches the verify hits into tokens (_predict_hits): for every
     branch key of every request, those tokens equal _predict's (every
     branch through the LM head at once) -- block with the anchor in its
-    first slot, and top-(A+1)."""
+    first slot, and top-(A+1).  Six requests make two prediction groups of
+    the four-request micro-batch, with hits in only some of the requests."""
     from d3d_amd.model import Sequence
     eng = _engine(29, anchor_num=2)
     g = torch.Generator().manual_seed(13)
     seqs = []
-    for i, n in enumerate((21, 34, 27)):
+    for i, n in enumerate(lens):
         s = Sequence(i, torch.randint(0, 999, (n,), generator=g).tolist())
         s.prefix = n
         s.needs_fast_seed = False
@@ -242,21 +244,28 @@ def test_lazy_hit_branches_equal_the_full_prediction():
     pending = eng._predict_submit(seqs, lazy=True)
     specs = {s.seq_id: e[1][b] for e in pending for b, s in enumerate(e[0])}
     checked = 0
-    for j in range(2 * 15 + 1):  # every branch position, one key per request each round
+    if len(lens) > eng.micro:
+        assert len(pending) == 2
+    for j in range(2 * 15 + 1):  # every branch position, one key per hit request each round
+        hitting = [i for i in range(len(seqs)) if (i + j) % every == 0]
         hits = []
-        for s in seqs:
+        for i in hitting:
+            s = seqs[i]
             key = specs[s.seq_id][j]
             hits.append((s, key, key[1] if key[1] is not None else 123))
         out = eng._predict_hits(pending, hits)
         eng._apply_hits(hits, out)
-        for (s, key, anchor), (cur, top) in zip(hits, saved):
+        for i, (s, key, anchor) in zip(hitting, hits):
+            cur, top = saved[i]
             block, want_top = full[s.seq_id][key]
             want = list(block)
             want[0] = anchor
             assert s.current == want and s.top == want_top, (s.seq_id, key)
             s.current, s.top = list(cur), [list(t) for t in top]
             checked += 1
-    assert checked == 3 * 31
+        for i in set(range(len(seqs))) - set(hitting):  # a request that missed keeps its block
+            assert (seqs[i].current, seqs[i].top) == saved[i]
+    assert checked == sum(1 for j in range(31) for i in range(len(seqs)) if (i + j) % every == 0)
     for s in seqs:
         eng.target.release(s)
         eng.draft.release(s)
