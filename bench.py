@@ -41,7 +41,10 @@ boundary and two dependent ones cost in the same graph harness.
 bytes those steps stream per call against the time they take.  ``value``
 times ``--steps`` new tokens per request (``config.new_tokens``); when that
 is not the configuration's 512, ``e2e_config_run`` reports the 512-token
-run beside it.
+run beside it.  ``e2e_all_accepted`` runs the same loop with both LM heads
+zeroed, so that every drafted token is accepted and the predicted
+all-accepted branch hits every verify: the engine's hit path, 16 tokens per
+request and step (random weights give the miss path: one token per step).
 
 ``roofline`` (the top-level object) is the batch-8 fused acceptance, the
 acceptance kernel at the size where its HBM efficiency is decided.
@@ -544,12 +547,20 @@ def draft_block_bench(dev, reps: int = 20):
     return ms
 
 
-def e2e_bench(dev, new_tokens: int, warm_tokens: int):
+def e2e_bench(dev, new_tokens: int, warm_tokens: int, all_accepted: bool = False):
     """Qwen3-8B-shaped target + Qwen3-1.7B-shaped draft co-resident, two streams:
-    batch 4, prompts of 512 random ids, greedy, 16-token blocks, 16-token pages."""
+    batch 4, prompts of 512 random ids, greedy, 16-token blocks, 16-token pages.
+
+    ``all_accepted`` zeroes both LM heads: every logit is 0, every greedy
+    token id 0, so the target accepts every drafted token and the packed
+    prediction's all-accepted branch matches every verify (the hit path:
+    no recovery forward, 16 tokens committed per request and step)."""
     from d3d_amd.engine import Engine
     from d3d_amd.model import D3D_1P7B, QWEN3_8B
     eng = Engine(QWEN3_8B, D3D_1P7B, anchor_num=1, pages=64, seed=42, tuned_gemms=True)
+    if all_accepted:
+        for r in (eng.target, eng.draft):
+            r.model.lm_head.zero_()
     g = torch.Generator().manual_seed(9)
     prompts = torch.randint(0, 151936, (4, 512), generator=g).tolist()
     # The warm-up captures the block graphs at the timed run's page-table
@@ -803,6 +814,19 @@ def main():
                 "note": "the configuration's full output length (contexts grow from 512 to 1024 tokens)",
             }
             print("engine loop timed at the configuration's output length", file=sys.stderr, flush=True)
+        acc = e2e_bench(dev, CONFIG_NEW_TOKENS, args.warmup, all_accepted=True)
+        out["e2e_all_accepted"] = {
+            "new_tokens": CONFIG_NEW_TOKENS, "steps": acc["steps"],
+            "steps_per_s": round(acc["steps_per_s"], 2), "ms_per_step": round(1e3 / acc["steps_per_s"], 3),
+            "tokens_per_s": round(acc["output_tokens"] / acc["elapsed_s"], 1),
+            "hits_per_request": [o["hits"] for o in acc["outputs"]],
+            "verify_ms": round(acc["verify_ms"], 3), "draft_ms": round(acc["draft_ms"], 3),
+            "overlap_fraction": round(acc["overlap_fraction"], 3),
+            "note": "both LM heads zeroed: every drafted token is accepted and the all-accepted predicted "
+                    "branch hits every verify, so steps run the hit path (no recovery forward) and commit "
+                    "16 tokens per request; not the headline",
+        }
+        print("engine loop timed with every block accepted", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_engine_step()
         out["cpu_baselines"] = cpu_baselines()

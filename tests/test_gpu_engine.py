@@ -138,6 +138,23 @@ def test_fast_backups_stay_lossless(backup):
     _same_up_to_near_tie(W, prompts, [o["tokens"] for o in want["outputs"]], [o["tokens"] for o in got["outputs"]])
 
 
+def test_all_accepted_blocks_continue_from_the_hit_branch():
+    """With both LM heads zeroed every logit is 0 and every greedy token is
+    id 0 (the first maximum): the target accepts every drafted token, the
+    packed prediction's all-accepted branch matches the verify, and
+    generate continues from that branch's block (a hit) instead of a
+    recovery forward.  The output is still the target's greedy decoding."""
+    eng = _engine(31)
+    for r in (eng.target, eng.draft):
+        r.model.lm_head.zero_()
+    prompts = torch.randint(0, 999, (3, 20), generator=torch.Generator().manual_seed(3)).tolist()
+    res = eng.generate(prompts, 3, max_new_tokens=40, ignore_eos=True)
+    assert all(o["tokens"] == [0] * 40 for o in res["outputs"])
+    assert all(o["hits"] >= 1 for o in res["outputs"])
+    ar = generate_ar(eng.target, prompts, 3, 40, ignore_eos=True)
+    assert [o["tokens"] for o in ar["outputs"]] == [o["tokens"] for o in res["outputs"]]
+
+
 def test_a_dropped_engine_frees_its_graphs_by_reference_counting():
     """Runners and their captured steps form no reference cycle: dropping
     an engine frees its graphs at once, with the cyclic collector off, so no
