@@ -109,6 +109,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-models", action="store_true",
                     help="kernel microbenchmarks only (no 1.7B draft-block or 8B + 1.7B engine run)")
+    ap.add_argument("--no-hit-path", action="store_true",
+                    help="skip the engine run with every block accepted (so a trace ends in the miss path)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain 64 MiB device copy 5 times (the reference kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -814,6 +816,7 @@ def main():
                 "note": "the configuration's full output length (contexts grow from 512 to 1024 tokens)",
             }
             print("engine loop timed at the configuration's output length", file=sys.stderr, flush=True)
+    if not args.no_models and not args.no_hit_path:
         acc = e2e_bench(dev, CONFIG_NEW_TOKENS, args.warmup, all_accepted=True)
         out["e2e_all_accepted"] = {
             "new_tokens": CONFIG_NEW_TOKENS, "steps": acc["steps"],
