@@ -9,9 +9,10 @@ operands and keeps the fastest; ``tune`` does that for the engine's step
 shapes and writes the results file, ``enable`` makes torch use the file's
 choices (tuning itself stays off, so no shape is timed at run time and
 shapes the file does not list keep the default solution).  The packed
-predict's qkv and down projections are the exception: they run beside the
-verify, and the file lists them on the library default, which slows the
-verify less than their fastest-alone choices (``corun_default_shapes``).
+predict's qkv and down projections and the verify's gate-up are the
+exception: the two forwards run side by side, and the file lists these on
+the library default, which slows the other stream less than their
+fastest-alone choices (``corun_default_shapes``).
 
 The choice changes the solution, not the operation: outputs stay within the
 usual bf16 GEMM rounding of one another, not bit-equal across solutions.
@@ -70,22 +71,25 @@ def step_gemm_shapes(target, draft, block: int = 16, batches: Iterable[int] = (1
 
 def corun_default_shapes(target, draft, block: int = 16, batches: Iterable[int] = (1, 2, 3, 4),
                          anchors: Iterable[int] = (1, 3)) -> List[Tuple[int, int, int]]:
-    """The packed predict's qkv and down projections, which keep the
-    library heuristic's default solution ("Default" in the results file)
-    instead of the fastest one alone.
+    """The shapes that keep the library heuristic's default solution
+    ("Default" in the results file) instead of the fastest one alone: the
+    packed predict's qkv and down projections and the verify's gate-up.
 
-    The packed predict runs beside the verify on the other stream.  Its
-    fastest-alone solutions for these two shapes slow the verify's 64-row
-    projections more than they gain: beside a loop of the tuned 1088-row
-    qkv, the target's o projection takes 20.3 us a call against 16.4 beside
-    the default (10.1 alone).  Engine loop (B=4, A=1, 96 new tokens, twelve
-    runs each, alternating processes on one box): 86.2-86.9 steps/s with
-    the tuned choices, 88.0-88.8 with these two on the default."""
+    The packed predict and the verify run side by side on the two streams,
+    and these fastest-alone choices slow the other stream more than they
+    gain.  Beside a loop of the tuned 1088-row qkv, the target's o
+    projection takes 20.3 us a call against 16.4 beside the default (10.1
+    alone).  Engine loop (B=4, A=1, 96 new tokens, twelve runs each,
+    alternating processes on one box): 86.2-86.9 steps/s with every shape
+    tuned, 88.0-88.8 with the predict qkv and down on the default; then,
+    on another box, 89.4-90.1 against 90.2-90.8 with the verify's gate-up
+    on the default as well."""
     out = set()
+    q, kv = draft.heads * draft.head_dim, draft.kv_heads * draft.head_dim
     for b in batches:
+        out.add((b * block, 2 * target.mlp, target.hidden))
         for A in anchors:
             Mp = b * block * (2 + A * (block - 1))
-            q, kv = draft.heads * draft.head_dim, draft.kv_heads * draft.head_dim
             out.update({(Mp, q + 2 * kv, draft.hidden), (Mp, draft.hidden, draft.mlp)})
     return sorted(out)
 

@@ -63,17 +63,19 @@ def test_enable_without_a_gpu_leaves_torch_defaults(tmp_path):
     assert gemm_tuning.enable(tmp_path / "missing.csv") is False
 
 
-def test_packed_predict_qkv_and_down_stay_on_the_library_default():
-    """The packed predict's qkv and down projections run beside the verify;
-    the file keeps them on the default solution, every other shape on a
-    timed choice (which may also be the default)."""
+def test_corun_shapes_stay_on_the_library_default():
+    """The packed predict's qkv and down projections and the verify's
+    gate-up run beside the other forward; the file keeps them on the default
+    solution, every other shape on a timed choice (which may also be the
+    default)."""
     _, res = _rows()
     sol = {}
     for _, params, solution, _ in res:
         N, M, K = map(int, params.split("_")[1:4])
         sol[(M, N, K)] = solution
     keep = gemm_tuning.corun_default_shapes(QWEN3_8B, D3D_1P7B)
-    assert len(keep) == 16 and set(keep) <= set(sol)
+    assert len(keep) == 20 and set(keep) <= set(sol)
     assert all(sol[s] == "Default" for s in keep)
-    assert (1088, 4096, 2048) in keep and (1088, 2048, 6144) in keep
+    assert (1088, 4096, 2048) in keep and (1088, 2048, 6144) in keep and (64, 24576, 4096) in keep
     assert (1088, 12288, 2048) not in keep and (1088, 2048, 2048) not in keep
+    assert (64, QWEN3_8B.vocab, 4096) not in keep
