@@ -181,7 +181,7 @@ def write_defaults(path: Path, shapes: Sequence[Tuple[int, int, int]], log=print
     ``path`` (replacing their lines, or adding them), each with its
     milliseconds per call timed on one operand set (cache-warm, unlike the
     tuner's rotating operands; the figure is informational)."""
-    lines = Path(path).read_text().splitlines()
+    lines = [l for l in Path(path).read_text().splitlines() if l.strip()]
     keys = {f"tn_{N}_{M}_{K}_ld_{K}_{K}_{N}": (M, N, K) for M, N, K in shapes}
     kept = [l for l in lines if l.startswith("Validator,") or l.split(",")[1] not in keys]
     res = [l for l in kept if not l.startswith("Validator,")]
