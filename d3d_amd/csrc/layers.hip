@@ -228,15 +228,10 @@ __global__ __launch_bounds__(NT) void qk_rope_append_kernel(
     dst[lane + 64] = (uint16_t)(ob >> 16);
 }
 
-// out[t, i] = silu(gate[t, i]) * up[t, i] with gate_up = [gate | up] per row.
-__global__ __launch_bounds__(NT) void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
-                                                      int M, size_t total_vec) {
-    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
-    if (i >= total_vec) return;
-    const int mv = M / 8;
-    const size_t t = i / mv, c = i % mv;
-    const u32x4 g = *reinterpret_cast<const u32x4*>(gu + t * 2 * M + c * 8);
-    const u32x4 u = *reinterpret_cast<const u32x4*>(gu + t * 2 * M + M + c * 8);
+// silu(g) * u of 8 bf16 columns (16-byte vectors).
+__device__ __forceinline__ void silu_mul_vec(const uint16_t* gp, const uint16_t* up, uint16_t* op) {
+    const u32x4 g = *reinterpret_cast<const u32x4*>(gp);
+    const u32x4 u = *reinterpret_cast<const u32x4*>(up);
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -249,7 +244,20 @@ __global__ __launch_bounds__(NT) void silu_mul_kernel(const uint16_t* __restrict
         }
         o[h] = pack2(r[0], r[1]);
     }
-    *reinterpret_cast<u32x4*>(out + t * M + c * 8) = o;
+    *reinterpret_cast<u32x4*>(op) = o;
+}
+
+// out[t, i] = silu(gate[t, i]) * up[t, i] with gate_up = [gate | up] per row.
+// Thread (x, y) takes 8-column vector x of rows y, y + gridDim.y, ... (no
+// per-thread division).
+__global__ __launch_bounds__(NT) void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                      int M, int T) {
+    const int c = blockIdx.x * NT + threadIdx.x;
+    if (c >= M / 8) return;
+    for (int t = blockIdx.y; t < T; t += gridDim.y) {
+        silu_mul_vec(gu + (size_t)t * 2 * M + (size_t)c * 8, gu + (size_t)t * 2 * M + M + (size_t)c * 8,
+                     out + (size_t)t * M + (size_t)c * 8);
+    }
 }
 
 }  // namespace layers
@@ -360,10 +368,9 @@ extern "C" int d3d_silu_mul(const void* gate_up, void* out, int T, int M, void* 
     if (T == 0) return D3D_OK;
     if (!gate_up || !out) return D3D_E_NULL;
     if (unaligned16(gate_up) || unaligned16(out)) return D3D_E_UNSUPPORTED;
-    const size_t total = (size_t)T * (M / 8);
-    const unsigned grid = (unsigned)((total + layers::NT - 1) / layers::NT);
-    hipLaunchKernelGGL(layers::silu_mul_kernel, dim3(grid), dim3(layers::NT), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), M, total);
+    const dim3 grid((unsigned)((M / 8 + layers::NT - 1) / layers::NT), (unsigned)(T < 65535 ? T : 65535));
+    hipLaunchKernelGGL(layers::silu_mul_kernel, grid, dim3(layers::NT), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), M, T);
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? D3D_OK : (int)err;
 }
