@@ -177,8 +177,10 @@ def test_qk_rope_position_zero_is_norm_only():
         _ulp_close(q, ref, max_ulp=1)
 
 
-@pytest.mark.parametrize("T,M", [(1, 6144), (128, 12288), (7, 8)])
+@pytest.mark.parametrize("T,M", [(1, 6144), (128, 12288), (7, 8), (1088, 6144), (70000, 8), (3, 2056)])
 def test_silu_mul(T, M):
+    """Rows past the launch's 65,535 grid rows (T = 70000) are taken by the
+    grid-stride loop; M = 2056 leaves a partial workgroup of vectors."""
     g = torch.Generator().manual_seed(T + M)
     gu = (torch.randn(T, 2 * M, generator=g) * 4).to(BF)
     out = ly.silu_mul(gu.to(DEV))
